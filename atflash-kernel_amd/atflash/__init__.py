@@ -1,0 +1,25 @@
+"""atflash for AMD MI355X: per-RoPE-wavelength windowed attention.
+
+    window_table    the rule: per-pair widths, D_eff per tile, slice statistics
+                    (same API as the reference's atflash/window_table.py)
+    atflash_window  torch-free twin that emits the kernels' level table `zhi`
+    fiwin_common    decode-side tables (vec8 slices, s-bar)
+    rope            RoPE tables for RoPE-at-load
+    cache           paged KV cache in the kernels' level-blocked layout
+    ops             torch.library operators over the HIP C ABI
+    interface       reference-shaped entry points (_flash_attn_fwd, decode)
+
+Importing the package does not load the HIP library; the first GPU call does,
+and fails loudly if it is missing.  The fp32 reference attention is test
+infrastructure and lives outside the package (oracle/ at the repository root).
+"""
+from . import atflash_window, fiwin_common, window_table
+
+__all__ = ["window_table", "atflash_window", "fiwin_common", "rope", "cache", "ops", "interface"]
+
+
+def __getattr__(name):
+    if name in ("rope", "cache", "ops", "interface"):
+        import importlib
+        return importlib.import_module(f".{name}", __name__)
+    raise AttributeError(name)

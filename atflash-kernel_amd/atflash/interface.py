@@ -1,0 +1,109 @@
+"""Entry points shaped like the reference's kernel interfaces.
+
+prefill  `_flash_attn_fwd(q, k, v, causal=True, pack_gqa=..., atflash_window_zhi=zhi)`
+         as called on the FA4 window port (microbench/b1_correctness.py:84-85,
+         e2e_pipeline/atflash_e2e_fafi.py:118-119): BSHD q [B, Nq, Hq, 128],
+         k/v [B, Nk, Hkv, 128] (strided views accepted), causal, bottom-right
+         aligned when Nq < Nk; window table absent = plain causal attention.
+decode   `single_decode_with_kv_cache(q, k, v, maybe_zhi=...)` as the FlashInfer
+         port's single-request decode (kernels/flashinfer_port/fiwin_common.py:96-112):
+         q [Hq, 128], k/v NHD [N, Hkv, 128] or HND [Hkv, N, 128].
+paged    `prefill_paged` / `decode_paged` on a PagedKVCache, the serving path.
+
+Differences from the reference that a caller sees:
+  * the window table is the 16-dim level table zhi for both prefill and decode
+    (decode quantizes it per 16-token page, block_n = 16);
+  * inputs may stay in the half-split (HF rotate_half) layout and RoPE can be
+    fused (`rope=` a table from atflash.rope.rope_table); the reference's
+    wavelength-sorted layout is accepted with layout="sorted_pair" and rope=None.
+"""
+import math
+
+import torch
+
+from . import _lib, ops
+from .cache import PAGE
+
+LAYOUTS = {"half_split": _lib.LAYOUT_HALF_SPLIT, "sorted_pair": _lib.LAYOUT_SORTED_PAIR}
+
+
+def _layout_id(layout):
+    if isinstance(layout, int):
+        return layout
+    if layout not in LAYOUTS:
+        raise ValueError(f"layout must be one of {sorted(LAYOUTS)}")
+    return LAYOUTS[layout]
+
+
+def _zhi_list(zhi):
+    if zhi is None:
+        return None
+    vals = [int(x) for x in (zhi.tolist() if isinstance(zhi, torch.Tensor) else zhi)]
+    if len(vals) != _lib.LEVELS:
+        raise ValueError(f"window table must have {_lib.LEVELS} entries, got {len(vals)}")
+    return vals
+
+
+def pack_kv(k, v, rope=None, layout="half_split", start_pos=0):
+    """Write contiguous-sequence k/v [B, N, Hkv, 128] into a fresh paged cache with
+    an identity page table.  Returns (k_cache, v_cache, page_table)."""
+    B, N, Hkv, D = k.shape
+    pages = -(-(int(start_pos) + N) // PAGE)
+    k_cache = torch.empty((B * pages, Hkv, _lib.LEVELS, PAGE, 16), dtype=torch.bfloat16, device=k.device)
+    v_cache = torch.empty((B * pages, Hkv, D, PAGE), dtype=torch.bfloat16, device=k.device)
+    page_table = torch.arange(B * pages, dtype=torch.int32, device=k.device).view(B, pages)
+    starts = torch.full((B,), int(start_pos), dtype=torch.int32, device=k.device)
+    ops.kv_write(k_cache, v_cache, k, v, starts, page_table, rope, _layout_id(layout))
+    return k_cache, v_cache, page_table
+
+
+def _flash_attn_fwd(q, k, v, causal=True, pack_gqa=None, atflash_window_zhi=None, softmax_scale=None,
+                    rope=None, layout="half_split", q_offset=None):
+    """Windowed causal GQA prefill.  Returns (out [B, Nq, Hq, 128] bf16,
+    lse [B, Hq, Nq] fp32).  pack_gqa is accepted for interface compatibility;
+    the tile quantization does not depend on it (block_m = 64 positions)."""
+    if not causal:
+        raise ValueError("only causal attention is supported")
+    B, Nq, Hq, D = q.shape
+    Nk = k.shape[1]
+    if D != _lib.HEAD_DIM or k.shape[-1] != D or v.shape != k.shape:
+        raise ValueError("q, k, v must have head_dim 128 and k, v equal shapes")
+    if Hq % k.shape[2] != 0:
+        raise ValueError("num q heads must be a multiple of num kv heads")
+    if Nq > Nk:
+        raise ValueError(f"L>S invalid: Nq={Nq} Nk={Nk}")
+    scale = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
+    k_cache, v_cache, table = pack_kv(k, v, rope=rope, layout=layout)
+    off = Nk - Nq if q_offset is None else int(q_offset)
+    return ops.prefill(q, k_cache, v_cache, table, Nk, off, _zhi_list(atflash_window_zhi), scale, rope,
+                       _layout_id(layout))
+
+
+def single_decode_with_kv_cache(q, k, v, maybe_zhi=None, sm_scale=None, kv_layout="NHD", rope=None,
+                                layout="half_split"):
+    """One query token per q head against a contiguous KV (convenience path: the
+    KV is packed into a temporary paged cache first).  Returns o [Hq, 128] bf16."""
+    if kv_layout == "HND":
+        k, v = k.transpose(0, 1), v.transpose(0, 1)
+    elif kv_layout != "NHD":
+        raise ValueError("kv_layout must be NHD or HND")
+    N = k.shape[0]
+    scale = 1.0 / math.sqrt(q.shape[-1]) if sm_scale is None else float(sm_scale)
+    k_cache, v_cache, table = pack_kv(k.unsqueeze(0), v.unsqueeze(0), rope=rope, layout=layout)
+    seq = torch.tensor([N], dtype=torch.int32, device=q.device)
+    o = ops.decode_paged(q.unsqueeze(0), k_cache, v_cache, table, seq, N, _zhi_list(maybe_zhi), scale, rope,
+                         _layout_id(layout))
+    return o[0]
+
+
+def prefill_paged(q, cache, page_table, nk, q_offset, zhi=None, sm_scale=None, rope=None, layout="half_split"):
+    scale = 1.0 / math.sqrt(q.shape[-1]) if sm_scale is None else float(sm_scale)
+    return ops.prefill(q, cache.k, cache.v, page_table, int(nk), int(q_offset), _zhi_list(zhi), scale, rope,
+                       _layout_id(layout))
+
+
+def decode_paged(q, cache, page_table, seq_lens, max_seq_len, zhi=None, sm_scale=None, rope=None,
+                 layout="half_split"):
+    scale = 1.0 / math.sqrt(q.shape[-1]) if sm_scale is None else float(sm_scale)
+    return ops.decode_paged(q, cache.k, cache.v, page_table, seq_lens, int(max_seq_len), _zhi_list(zhi), scale,
+                            rope, _layout_id(layout))

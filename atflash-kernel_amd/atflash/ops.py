@@ -1,0 +1,165 @@
+"""torch.library operators over the C ABI (namespace `atflash`).
+
+    torch.ops.atflash.kv_write(k_cache, v_cache, k, v, start_pos, page_table, rope_cs, layout)
+    torch.ops.atflash.prefill(q, k_cache, v_cache, page_table, nk, q_offset, zhi, sm_scale,
+                              rope_cs, layout) -> (out, lse)
+    torch.ops.atflash.decode_paged(q, k_cache, v_cache, page_table, seq_lens, max_seq_len, zhi,
+                                   sm_scale, rope_cs, layout) -> out
+
+Each op checks shapes and dtypes, then calls the HIP library on the current
+stream of the tensors' device.  There is no CPU or PyTorch fallback: a CPU
+tensor or a missing library is an error.
+"""
+from typing import List, Optional, Tuple
+
+import torch
+
+from . import _lib
+
+
+def _need_gpu(*ts):
+    for t in ts:
+        if t is not None and t.device.type != "cuda":
+            raise ValueError("atflash ops run on the GPU only (got a tensor on %s)" % t.device)
+
+
+def _need(cond, msg):
+    if not cond:
+        raise ValueError(msg)
+
+
+def _check_cache(k_cache, v_cache):
+    _need(k_cache.dtype == torch.bfloat16 and v_cache.dtype == torch.bfloat16, "caches must be bf16")
+    _need(k_cache.dim() == 5 and tuple(k_cache.shape[2:]) == (_lib.LEVELS, _lib.PAGE_SIZE, 16),
+          "k_cache must be [num_pages, num_kv_heads, 8, 16, 16]")
+    _need(v_cache.shape == (k_cache.shape[0], k_cache.shape[1], _lib.HEAD_DIM, _lib.PAGE_SIZE),
+          "v_cache must be [num_pages, num_kv_heads, 128, 16]")
+    _need(k_cache.is_contiguous() and v_cache.is_contiguous(), "caches must be contiguous")
+
+
+def _layout(layout: int) -> int:
+    _need(layout in (_lib.LAYOUT_HALF_SPLIT, _lib.LAYOUT_SORTED_PAIR), f"unknown layout {layout}")
+    return layout
+
+
+def _rope(rope_cs):
+    if rope_cs is None:
+        return None, 0
+    _need(rope_cs.dtype == torch.float32 and rope_cs.dim() == 3 and rope_cs.shape[1:] == (_lib.HEAD_DIM // 2, 2)
+          and rope_cs.is_contiguous(), "rope_cs must be contiguous fp32 [max_pos, 64, 2]")
+    return rope_cs, rope_cs.shape[0]
+
+
+@torch.library.custom_op("atflash::kv_write", mutates_args=("k_cache", "v_cache"))
+def kv_write(k_cache: torch.Tensor, v_cache: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+             start_pos: torch.Tensor, page_table: torch.Tensor, rope_cs: Optional[torch.Tensor],
+             layout: int) -> None:
+    """Write k/v [B, T, Hkv, 128] (token t of sequence b at absolute position
+    start_pos[b] + t) into the paged cache, rotating K with rope_cs."""
+    _need_gpu(k_cache, v_cache, k, v, start_pos, page_table, rope_cs)
+    _check_cache(k_cache, v_cache)
+    _need(k.dtype == torch.bfloat16 and v.dtype == torch.bfloat16, "k and v must be bf16")
+    _need(k.dim() == 4 and k.shape == v.shape and k.shape[-1] == _lib.HEAD_DIM,
+          "k and v must be [B, T, Hkv, 128] of equal shape")
+    _need(k.shape[2] == k_cache.shape[1], "k heads must equal the cache's kv heads")
+    _need(k.stride(-1) == 1 and v.stride(-1) == 1, "last dim of k and v must be contiguous")
+    _need(start_pos.dtype == torch.int32 and start_pos.numel() == k.shape[0], "start_pos must be int32 [B]")
+    _need(page_table.dtype == torch.int32 and page_table.dim() == 2 and page_table.shape[0] == k.shape[0]
+          and page_table.is_contiguous(), "page_table must be contiguous int32 [B, max_pages]")
+    rope_cs, max_pos = _rope(rope_cs)
+    L = _lib.lib()
+    _lib.check(L.atf_kv_write_bf16(
+        _lib.ptr(k_cache), _lib.ptr(v_cache), k_cache.shape[0], k_cache.shape[1],
+        _lib.ptr(k), k.stride(0), k.stride(1), k.stride(2),
+        _lib.ptr(v), v.stride(0), v.stride(1), v.stride(2),
+        k.shape[0], k.shape[1], _lib.ptr(start_pos.contiguous()), _lib.ptr(page_table), page_table.shape[1],
+        _lib.ptr(rope_cs), max_pos, _layout(layout), _lib.stream_of(k.device)))
+
+
+@kv_write.register_fake
+def _(k_cache, v_cache, k, v, start_pos, page_table, rope_cs, layout):
+    return None
+
+
+@torch.library.custom_op("atflash::prefill", mutates_args=())
+def prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, page_table: torch.Tensor,
+            nk: int, q_offset: int, zhi: Optional[List[int]], sm_scale: float,
+            rope_cs: Optional[torch.Tensor], layout: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Windowed causal GQA prefill of q [B, Nq, Hq, 128] (absolute positions
+    q_offset..q_offset+Nq-1) against nk cached keys.  Returns (out bf16
+    [B, Nq, Hq, 128], lse fp32 [B, Hq, Nq])."""
+    _need_gpu(q, k_cache, v_cache, page_table, rope_cs)
+    _check_cache(k_cache, v_cache)
+    _need(q.dtype == torch.bfloat16 and q.dim() == 4 and q.shape[-1] == _lib.HEAD_DIM,
+          "q must be bf16 [B, Nq, Hq, 128]")
+    _need(q.stride(-1) == 1, "last dim of q must be contiguous")
+    _need(page_table.dtype == torch.int32 and page_table.dim() == 2 and page_table.shape[0] == q.shape[0]
+          and page_table.is_contiguous(), "page_table must be contiguous int32 [B, max_pages]")
+    B, Nq, Hq, _ = q.shape
+    rope_cs, max_pos = _rope(rope_cs)
+    out = torch.empty((B, Nq, Hq, _lib.HEAD_DIM), dtype=torch.bfloat16, device=q.device)
+    lse = torch.empty((B, Hq, Nq), dtype=torch.float32, device=q.device)
+    L = _lib.lib()
+    _lib.check(L.atf_prefill_bf16(
+        _lib.ptr(out), out.stride(0), out.stride(1), out.stride(2), _lib.ptr(lse),
+        _lib.ptr(q), q.stride(0), q.stride(1), q.stride(2),
+        _lib.ptr(k_cache), _lib.ptr(v_cache), k_cache.shape[0], _lib.ptr(page_table), page_table.shape[1],
+        B, Nq, int(nk), int(q_offset), Hq, k_cache.shape[1], _lib.zhi_array(zhi), float(sm_scale),
+        _lib.ptr(rope_cs), max_pos, _layout(layout), _lib.stream_of(q.device)))
+    return out, lse
+
+
+@prefill.register_fake
+def _(q, k_cache, v_cache, page_table, nk, q_offset, zhi, sm_scale, rope_cs, layout):
+    B, Nq, Hq, D = q.shape
+    return q.new_empty((B, Nq, Hq, D)), q.new_empty((B, Hq, Nq), dtype=torch.float32)
+
+
+@torch.library.custom_op("atflash::decode_paged", mutates_args=())
+def decode_paged(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, page_table: torch.Tensor,
+                 seq_lens: torch.Tensor, max_seq_len: int, zhi: Optional[List[int]], sm_scale: float,
+                 rope_cs: Optional[torch.Tensor], layout: int) -> torch.Tensor:
+    """Windowed split-KV decode of q [B, Hq, 128] (query of sequence b at
+    position seq_lens[b] - 1).  Returns out bf16 [B, Hq, 128]."""
+    _need_gpu(q, k_cache, v_cache, page_table, seq_lens, rope_cs)
+    _check_cache(k_cache, v_cache)
+    _need(q.dtype == torch.bfloat16 and q.dim() == 3 and q.shape[-1] == _lib.HEAD_DIM,
+          "q must be bf16 [B, Hq, 128]")
+    _need(q.stride(-1) == 1, "last dim of q must be contiguous")
+    _need(seq_lens.dtype == torch.int32 and seq_lens.numel() == q.shape[0], "seq_lens must be int32 [B]")
+    _need(page_table.dtype == torch.int32 and page_table.dim() == 2 and page_table.shape[0] == q.shape[0]
+          and page_table.is_contiguous(), "page_table must be contiguous int32 [B, max_pages]")
+    B, Hq, _ = q.shape
+    hkv = k_cache.shape[1]
+    rope_cs, max_pos = _rope(rope_cs)
+    L = _lib.lib()
+    nbytes = int(L.atf_decode_workspace_bytes(B, Hq, hkv, int(max_seq_len)))
+    ws = torch.empty((max(nbytes, 16) + 3) // 4, dtype=torch.float32, device=q.device)
+    out = torch.empty((B, Hq, _lib.HEAD_DIM), dtype=torch.bfloat16, device=q.device)
+    _lib.check(L.atf_decode_paged_bf16(
+        _lib.ptr(out), out.stride(0), out.stride(1), _lib.ptr(q), q.stride(0), q.stride(1),
+        _lib.ptr(k_cache), _lib.ptr(v_cache), k_cache.shape[0], _lib.ptr(page_table), page_table.shape[1],
+        _lib.ptr(seq_lens.contiguous()), B, Hq, hkv, int(max_seq_len), _lib.zhi_array(zhi), float(sm_scale),
+        _lib.ptr(rope_cs), max_pos, _layout(layout), _lib.ptr(ws), ws.numel() * 4, _lib.stream_of(q.device)))
+    return out
+
+
+@decode_paged.register_fake
+def _(q, k_cache, v_cache, page_table, seq_lens, max_seq_len, zhi, sm_scale, rope_cs, layout):
+    return q.new_empty(q.shape)
+
+
+def prefill_tile_levels(n_row_tiles: int, n_kblocks: int, q_offset: int, zhi, device="cuda") -> torch.Tensor:
+    """Level counts the prefill kernel uses per (64-row tile, 32-key block)."""
+    out = torch.empty((n_row_tiles, n_kblocks), dtype=torch.int32, device=device)
+    _lib.check(_lib.lib().atf_prefill_tile_levels(_lib.ptr(out), n_row_tiles, n_kblocks, q_offset,
+                                                  _lib.zhi_array(zhi), _lib.stream_of(out.device)))
+    return out
+
+
+def decode_page_levels(n_pages: int, seq_len: int, zhi, device="cuda") -> torch.Tensor:
+    """Level counts the decode kernel uses per page of a sequence of length seq_len."""
+    out = torch.empty((n_pages,), dtype=torch.int32, device=device)
+    _lib.check(_lib.lib().atf_decode_page_levels(_lib.ptr(out), n_pages, seq_len, _lib.zhi_array(zhi),
+                                                 _lib.stream_of(out.device)))
+    return out

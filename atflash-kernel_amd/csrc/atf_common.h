@@ -1,0 +1,145 @@
+// Shared definitions for the gfx950 windowed-attention kernels.
+//
+// Head dim and the window rule
+//   d = 128, P = d/2 = 64 RoPE pairs.  Pair r (standard order, r = 0 highest
+//   frequency) sits in dims (r, r+P) of the half-split ("rotate_half") layout.
+//   The window keeps the lowest-frequency pairs, a prefix in wavelength order, in
+//   16-dim levels: level l (0 = always kept) holds pairs r in [P-8(l+1), P-8l),
+//   i.e. dims [P-8(l+1), P-8l) and the same range + P.  In the sorted-pair
+//   layout of the reference (atflash/window_table.py:13-21) level l is simply
+//   dims [16l, 16l+16).
+//   D_eff(z) = 16 * #{i : zhi[i] >= z} (microbench/b1_correctness.py:43-44), with
+//   zhi the per-level table of window_tables/atflash_window.py:85-108; window OFF
+//   is zhi[i] = INT32_MAX, i.e. D_eff = d everywhere.
+//
+// Paged KV cache (one layer), page = 16 tokens, per (page, kv head):
+//   K block  [8 levels][16 tokens][16 dims] bf16 = 4096 B, RoPE already applied.
+//            Dims of a level are stored as [first-half 8 | second-half 8]
+//            (half-split) or [16l .. 16l+15] (sorted pair).  Levels are
+//            contiguous 512 B runs, so a page read for L levels is one
+//            contiguous 512*L-byte prefix of the block.
+//   V block  [128 dims][16 token slots] bf16 = 4096 B (V transposed), token t of
+//            the page stored in slot kVSlot(t); the slot order matches the lane
+//            layout of the 32x32x16 and 16x16x16 MFMA accumulators so that P never
+//            leaves registers.
+//   k_cache: [num_pages][num_kv_heads][4096 B], v_cache likewise.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace atf {
+
+constexpr int kD = 128;
+constexpr int kP = 64;
+constexpr int kLevels = 8;
+constexpr int kPage = 16;
+constexpr int kBlockElems = kLevels * kPage * 16;  // 2048 bf16 = 4096 B
+constexpr int kLayoutHalfSplit = 0;
+constexpr int kLayoutSortedPair = 1;
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+typedef __attribute__((ext_vector_type(4))) short s16x4;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
+
+// The per-level distance table, passed by value (kernel argument, lives in SGPRs).
+struct LevelTable {
+  int32_t zhi[kLevels];
+};
+
+// Number of 16-dim levels read at causal distance z (>= 1: D_eff is clamped to 16).
+__device__ __forceinline__ int levels_of(const LevelTable& t, int z) {
+  int n = 0;
+#pragma unroll
+  for (int i = 0; i < kLevels; ++i) n += (t.zhi[i] >= z) ? 1 : 0;
+  return n < 1 ? 1 : n;
+}
+
+// First dim of the two 8-dim chunks of level l.
+__device__ __forceinline__ int level_chunk0(int layout, int l) {
+  return layout == kLayoutHalfSplit ? kP - 8 * (l + 1) : 16 * l;
+}
+__device__ __forceinline__ int level_chunk1(int layout, int l) {
+  return layout == kLayoutHalfSplit ? 2 * kP - 8 * (l + 1) : 16 * l + 8;
+}
+
+// Slot of token t (0..15) inside a transposed V page: token groups of 4 are
+// stored in the order {0, 2, 1, 3}.
+__device__ __forceinline__ int v_slot(int t) {
+  const int g = t >> 2;
+  const int gs = (g == 1) ? 2 : (g == 2 ? 1 : g);
+  return 4 * gs + (t & 3);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// fp32 -> bf16, round to nearest even (finite inputs; NaN stays NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+}
+
+// Unpack 8 bf16 (16 B) into floats.
+__device__ __forceinline__ void unpack8(const u32x4& v, float* f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(v[i] << 16);
+    f[2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u);
+  }
+}
+
+__device__ __forceinline__ u32x4 pack8(const float* f) {
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = pack_bf16x2(f[2 * i], f[2 * i + 1]);
+  return r;
+}
+
+// Rotate-half RoPE on one 8-pair chunk: lane keeps the first half
+// (x1 c - x2 s) or the second half (x2 c + x1 s).  cs holds (cos, sin) per pair.
+__device__ __forceinline__ u32x4 rope_half(const u32x4& x1v, const u32x4& x2v, const float* cs,
+                                          bool second) {
+  float x1[8], x2[8], y[8];
+  unpack8(x1v, x1);
+  unpack8(x2v, x2);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float c = cs[2 * i], s = cs[2 * i + 1];
+    y[i] = second ? (x2[i] * c + x1[i] * s) : (x1[i] * c - x2[i] * s);
+  }
+  return pack8(y);
+}
+
+__device__ __forceinline__ u32x4 ldg16(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+
+__device__ __forceinline__ void load_cs8(const float* rope_cs, int pos, int pair0, float* cs) {
+  const u32x4* p = reinterpret_cast<const u32x4*>(rope_cs + (static_cast<size_t>(pos) * kP + pair0) * 2);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const u32x4 v = p[i];
+    cs[4 * i + 0] = __uint_as_float(v[0]);
+    cs[4 * i + 1] = __uint_as_float(v[1]);
+    cs[4 * i + 2] = __uint_as_float(v[2]);
+    cs[4 * i + 3] = __uint_as_float(v[3]);
+  }
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Exchange with lane ^ 32.
+__device__ __forceinline__ float swap32(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]);
+}
+
+}  // namespace atf

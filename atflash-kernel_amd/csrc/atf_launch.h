@@ -1,0 +1,94 @@
+// Kernel argument blocks and host-side launchers (one per kernel file).
+#pragma once
+#include "atf_common.h"
+
+namespace atf {
+
+// Prefill geometry (the oracle's tile quantization is block_m = kPfRowsWave
+// query positions by block_n = kPfWinN keys).
+constexpr int kPfWaves = 4;
+constexpr int kPfRowsWave = 64;
+constexpr int kPfRowsWg = kPfWaves * kPfRowsWave;
+constexpr int kPfTileN = 64;
+constexpr int kPfWinN = 32;
+constexpr int kPfStageBytes = 8 * 4096;  // 4 K pages + 4 V pages
+constexpr int kPfLdsBytes = 2 * kPfStageBytes;
+
+// Decode geometry (block_n = one page).
+constexpr int kDecMaxGroup = 16;
+constexpr int kDecUnroll = 4;
+
+struct KvWriteArgs {
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+  int num_pages, hkv;
+  const uint16_t* k_src;
+  const uint16_t* v_src;
+  int64_t ks_b, ks_t, ks_h, vs_b, vs_t, vs_h;
+  int batch, n_tokens;
+  const int32_t* start_pos;  // [batch], absolute position of source token 0
+  const int32_t* page_table;
+  int max_pages;
+  const float* rope_cs;
+  int rope_max_pos;
+  int layout;
+};
+
+struct PrefillArgs {
+  const uint16_t* q;
+  int64_t q_sb, q_st, q_sh;
+  uint16_t* out;
+  int64_t o_sb, o_st, o_sh;
+  float* lse;  // [B][Hq][nq] natural-log LSE, or null
+  const uint16_t* k_cache;
+  const uint16_t* v_cache;
+  int num_pages;
+  const int32_t* page_table;
+  int max_pages;
+  int batch, nq, nk, q_offset, hq, hkv, group;
+  int n_qtiles, n_qgroups;
+  float scale_log2;
+  float sm_scale;
+  const float* rope_cs;
+  int layout;
+  LevelTable lt;
+};
+
+struct DecodeArgs {
+  const uint16_t* q;  // [B][Hq][128] (strided)
+  int64_t q_sb, q_sh;
+  const uint16_t* k_cache;
+  const uint16_t* v_cache;
+  int num_pages;
+  const int32_t* page_table;
+  int max_pages;
+  const int32_t* seq_lens;
+  int max_seq_len;
+  int batch, hq, hkv, group;
+  int n_splits, pages_per_split;
+  float scale_log2;
+  const float* rope_cs;
+  int layout;
+  LevelTable lt;
+  float* ws_o;   // [B][Hkv][n_splits][16][128]
+  float* ws_ml;  // [B][Hkv][n_splits][16][2]
+};
+
+struct MergeArgs {
+  uint16_t* out;  // [B][Hq][128] (strided)
+  int64_t o_sb, o_sh;
+  const float* ws_o;
+  const float* ws_ml;
+  int batch, hq, hkv, group, n_splits;
+  float scale_log2;
+};
+
+hipError_t launch_kv_write(const KvWriteArgs& a, hipStream_t s);
+hipError_t launch_prefill(const PrefillArgs& a, hipStream_t s);
+hipError_t launch_prefill_tile_levels(int32_t* out, int n_row_tiles, int n_kblocks, int q_offset,
+                                      const LevelTable& lt, hipStream_t s);
+hipError_t launch_decode(const DecodeArgs& a, const MergeArgs& m, hipStream_t s);
+hipError_t launch_decode_page_levels(int32_t* out, int n_pages, int seq_len, const LevelTable& lt,
+                                     hipStream_t s);
+
+}  // namespace atf

@@ -1,0 +1,137 @@
+/*
+ * atflash C ABI: per-RoPE-wavelength windowed attention on AMD MI355X (gfx950).
+ *
+ * Plain pointers and sizes only.  Every tensor pointer is a device pointer
+ * (HIP), allocated and owned by the caller; `stream` is a hipStream_t passed as
+ * void* (NULL = default stream).  All work is enqueued asynchronously on
+ * `stream`; no entry point synchronises the device.  Every entry point returns
+ * ATF_OK (0) or an ATF_ERR_* code; atf_last_error() then describes the failure
+ * (per calling thread).
+ *
+ * Window tables.  `zhi` is a HOST array of ATF_LEVELS int32 entries: zhi[i] is
+ * the largest causal key distance at which 16-dim level i is still read
+ * (window_tables/atflash_window.py:85-108, capped at a value >= the longest
+ * causal distance of the call).  NULL means window OFF: plain causal attention,
+ * every level read at every distance.  Level l holds RoPE pairs
+ * r in [64-8(l+1), 64-8l) (dims r and r+64 of the half-split layout).
+ *
+ * Paged KV cache (one layer): pages of ATF_PAGE_SIZE = 16 tokens.
+ *   k_cache  bf16 [num_pages][num_kv_heads][8 levels][16 tokens][16 dims]
+ *   v_cache  bf16 [num_pages][num_kv_heads][128 dims][16 token slots]
+ * written by atf_kv_write_bf16 (RoPE applied to K there); page_table is int32
+ * [batch][max_pages] of page ids.  Token slots of a page that were never written
+ * may hold any finite value.
+ *
+ * RoPE.  rope_cs, when not NULL, is fp32 [rope_max_pos][64][2] holding
+ * (cos, sin) of position * inv_freq[r] (HF rotate-half convention); NULL means
+ * the inputs are already rotated.  Layout ATF_LAYOUT_SORTED_PAIR (the
+ * reference's wavelength-sorted layout) requires rope_cs == NULL.
+ */
+#ifndef ATFLASH_H_
+#define ATFLASH_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ATF_ABI_VERSION 1
+#define ATF_HEAD_DIM 128
+#define ATF_LEVELS 8
+#define ATF_PAGE_SIZE 16
+#define ATF_LAYOUT_HALF_SPLIT 0
+#define ATF_LAYOUT_SORTED_PAIR 1
+/* Tile quantization of the window (the block_m/block_n the oracle must use). */
+#define ATF_PREFILL_BLOCK_M 64
+#define ATF_PREFILL_BLOCK_N 32
+#define ATF_DECODE_BLOCK_N 16
+#define ATF_MAX_GQA_GROUP 16
+
+enum {
+  ATF_OK = 0,
+  ATF_ERR_INVALID = 1,     /* bad argument (shape, stride, alignment, table) */
+  ATF_ERR_UNSUPPORTED = 2, /* valid request this build does not support */
+  ATF_ERR_LAUNCH = 3,      /* HIP launch or runtime error */
+  ATF_ERR_WORKSPACE = 4    /* workspace missing or too small */
+};
+
+int atf_abi_version(void);
+const char* atf_last_error(void);
+
+/*
+ * Write n_tokens tokens of each of `batch` sequences into the paged cache.
+ * Source token t of sequence b sits at absolute position start_pos[b] + t
+ * (start_pos: device int32 [batch]) and goes to page
+ * page_table[b][pos / 16], slot pos % 16.  K is rotated with rope_cs at that
+ * position.  Source strides are in elements; the last dim is contiguous.
+ *
+ * Replaces the reference's RoPE + head-dim permutation patch and HF cache append
+ * (e2e_pipeline/atflash_e2e_fafi.py:186-192, 101-119).
+ */
+int atf_kv_write_bf16(void* k_cache, void* v_cache, int num_pages, int num_kv_heads,
+                      const void* k_src, int64_t ks_b, int64_t ks_t, int64_t ks_h,
+                      const void* v_src, int64_t vs_b, int64_t vs_t, int64_t vs_h,
+                      int batch, int n_tokens, const int32_t* start_pos,
+                      const int32_t* page_table, int max_pages,
+                      const float* rope_cs, int rope_max_pos, int layout, void* stream);
+
+/*
+ * Windowed causal GQA prefill: out[b, i, h, :] = attention of query row i
+ * (absolute position q_offset + i) over keys 0..q_offset+i of sequence b read
+ * from the paged cache (nk keys present, q_offset + nq <= nk).  q/out are bf16
+ * [batch][nq][num_q_heads][128] with element strides (last dim contiguous).
+ * lse (nullable) receives fp32 [batch][num_q_heads][nq] natural-log
+ * log-sum-exp of the scaled scores.  Q is rotated with rope_cs at load.
+ *
+ * Replaces flash_attn.cute.interface._flash_attn_fwd(q, k, v, causal=True,
+ * atflash_window_zhi=zhi) of the FA4 window port (call sites
+ * microbench/b1_correctness.py:84-85, e2e_pipeline/atflash_e2e_fafi.py:118-119).
+ */
+int atf_prefill_bf16(void* out, int64_t o_sb, int64_t o_st, int64_t o_sh, float* lse,
+                     const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh,
+                     const void* k_cache, const void* v_cache, int num_pages,
+                     const int32_t* page_table, int max_pages,
+                     int batch, int nq, int nk, int q_offset, int num_q_heads, int num_kv_heads,
+                     const int32_t* zhi, float sm_scale, const float* rope_cs, int rope_max_pos,
+                     int layout, void* stream);
+
+/* Bytes of fp32 workspace atf_decode_paged_bf16 needs for these sizes. */
+size_t atf_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int max_seq_len);
+
+/*
+ * Windowed split-KV decode: one query token per sequence at position
+ * seq_lens[b] - 1 attending to keys 0..seq_lens[b]-1 of the paged cache.
+ * q/out are bf16 [batch][num_q_heads][128] with element strides; seq_lens is a
+ * device int32 [batch] whose entries must not exceed max_seq_len.  The window
+ * is quantized per page (block_n = 16): page p reads its first L(p) levels only.
+ *
+ * Replaces flashinfer.decode.single_decode_with_kv_cache_with_jit_module(...,
+ * maybe_zhi_slice=...) of the FlashInfer window port
+ * (kernels/flashinfer_port/fiwin_common.py:96-112, e2e_pipeline/atflash_e2e_fafi.py:106-109).
+ */
+int atf_decode_paged_bf16(void* out, int64_t o_sb, int64_t o_sh,
+                          const void* q, int64_t q_sb, int64_t q_sh,
+                          const void* k_cache, const void* v_cache, int num_pages,
+                          const int32_t* page_table, int max_pages, const int32_t* seq_lens,
+                          int batch, int num_q_heads, int num_kv_heads, int max_seq_len,
+                          const int32_t* zhi, float sm_scale, const float* rope_cs, int rope_max_pos,
+                          int layout, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Per-tile level counts (D_eff / 16) as the kernels compute them, for tests of
+ * the integer window path.  prefill: out int32 [n_row_tiles][n_kblocks] for
+ * 64-row query tiles starting at q_offset + 64*i and 32-key blocks;
+ * decode: out int32 [n_pages] for a sequence of length seq_len.
+ * Mirror atflash/window_table.py deff_segments (79-102) at these tiles.
+ */
+int atf_prefill_tile_levels(int32_t* out, int n_row_tiles, int n_kblocks, int q_offset,
+                            const int32_t* zhi, void* stream);
+int atf_decode_page_levels(int32_t* out, int n_pages, int seq_len, const int32_t* zhi, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ATFLASH_H_ */

@@ -1,0 +1,126 @@
+"""Decode kernel parity against the fp32 oracle (GPU).
+
+Oracle: atflash/reference.py phase="decode" restated in oracle/attention.py, with
+the window quantized per 16-token page (block_n = 16), which is exactly the
+per-page level count the kernel uses to gate its K loads.
+"""
+import pytest
+import torch
+
+import helpers as H
+from oracle import window_rule as WR
+
+pytestmark = pytest.mark.gpu
+
+
+def _decode_single(q, k, v, base, k_ret, rope, dev):
+    from atflash import atflash_window as AW, interface, rope as R
+    N = k.shape[0]
+    zhi = None if k_ret is None else AW.window_zhi_from_kret(H.D, base, k_ret, max(N, 16))
+    rt = R.rope_table(N, R.inv_freq(H.D, base, dev)) if rope else None
+    o = interface.single_decode_with_kv_cache(q.to(dev), k.to(dev), v.to(dev), maybe_zhi=zhi, rope=rt)
+    torch.cuda.synchronize()
+    return o.cpu()
+
+
+CASES = [
+    # name, N, Hq, Hkv, base, k_ret, rope
+    ("len1", 1, 24, 8, 5e5, 2.0, True),
+    ("len15", 15, 24, 8, 5e5, 2.0, True),
+    ("len16", 16, 24, 8, 5e5, 2.0, True),
+    ("len17", 17, 24, 8, 5e5, 2.0, True),
+    ("llama_1000_k2", 1000, 24, 8, 5e5, 2.0, True),
+    ("llama_4096_off", 4096, 24, 8, 5e5, None, True),
+    ("qwen_g7_8192_k2", 8192, 28, 4, 1e7, 2.0, True),
+    ("qwen_g7_8192_k64", 8192, 28, 4, 1e7, 64.0, True),
+    ("c1_g4_prerotated", 2048, 4, 1, 1e4, 2.0, False),
+    ("narrow_window", 3000, 8, 2, 1e4, 0.3, True),
+]
+
+
+@pytest.mark.parametrize("name,N,hq,hkv,base,k_ret,rope", CASES, ids=[c[0] for c in CASES])
+def test_decode_matches_oracle(name, N, hq, hkv, base, k_ret, rope, dev):
+    print(f"[decode parity] {name} N={N} hq={hq} hkv={hkv} k={k_ret} rope={rope}", flush=True)
+    g = torch.Generator().manual_seed(1234 + N)
+    q = H.randn_bf16((hq, H.D), g)
+    k = H.randn_bf16((N, hkv, H.D), g)
+    v = H.randn_bf16((N, hkv, H.D), g)
+    out = _decode_single(q, k, v, base, k_ret, rope, dev)
+    ref = H.decode_oracle(q, k, v, base, float("inf") if k_ret is None else k_ret, rope)
+    mx, mean = H.assert_close(out, ref, name)
+    print(f"  max {mx:.3e} mean {mean:.3e}")
+
+
+def test_batched_paged_decode_random_pages(dev):
+    """C3-like: batch 8, ragged lengths, pages randomly permuted over a shared pool."""
+    from atflash import atflash_window as AW, interface, rope as R
+    from atflash.cache import PagedKVCache
+    base, hq, hkv = 5e5, 24, 8
+    lens = [1, 17, 300, 1024, 2049, 4000, 5555, 8192]
+    B = len(lens)
+    total_pages = sum(-(-n // 16) for n in lens) + 37
+    cache = PagedKVCache(total_pages, hkv, dev)
+    perm = torch.randperm(total_pages, generator=torch.Generator().manual_seed(7)).tolist()
+    cache._free = perm
+    maxlen = max(lens)
+    rt = R.rope_table(maxlen, R.inv_freq(H.D, base, dev))
+    zhi = AW.window_zhi_from_kret(H.D, base, 2.0, 1 << 20)
+    g = torch.Generator().manual_seed(99)
+    seqs = []
+    for b, n in enumerate(lens):
+        cache.add_sequence(b, n)
+        k = H.randn_bf16((1, n, hkv, H.D), g)
+        v = H.randn_bf16((1, n, hkv, H.D), g)
+        seqs.append((k, v))
+    table = cache.page_table(list(range(B)))
+    for b, (k, v) in enumerate(seqs):
+        tb = table[b:b + 1].contiguous()
+        torch.ops.atflash.kv_write(cache.k, cache.v, k.to(dev), v.to(dev),
+                                   torch.zeros(1, dtype=torch.int32, device=dev), tb, rt, 0)
+    q = H.randn_bf16((B, hq, H.D), g)
+    seq_lens = torch.tensor(lens, dtype=torch.int32, device=dev)
+    for z in (zhi, None):
+        out = interface.decode_paged(q.to(dev), cache, table, seq_lens, maxlen, zhi=z, rope=rt).cpu()
+        for b, (k, v) in enumerate(seqs):
+            ref = H.decode_oracle(q[b], k[0], v[0], base, 2.0 if z else float("inf"), True)
+            H.assert_close(out[b], ref, f"seq {b} len {lens[b]} window={'on' if z else 'off'}")
+
+
+def test_decode_off_equals_k_inf_bitwise(dev):
+    from atflash import atflash_window as AW
+    g = torch.Generator().manual_seed(5)
+    q = H.randn_bf16((24, H.D), g)
+    k = H.randn_bf16((3000, 8, H.D), g)
+    v = H.randn_bf16((3000, 8, H.D), g)
+    from atflash import interface
+    a = interface.single_decode_with_kv_cache(q.to(dev), k.to(dev), v.to(dev), maybe_zhi=None)
+    zinf = AW.window_zhi_from_kret(H.D, 5e5, float("inf"), 4096)
+    b = interface.single_decode_with_kv_cache(q.to(dev), k.to(dev), v.to(dev), maybe_zhi=zinf)
+    assert torch.equal(a.cpu(), b.cpu())
+
+
+def test_page_levels_match_oracle_segments(dev):
+    from atflash import atflash_window as AW, ops
+    for base, k_ret, N in [(1e7, 2.0, 131072), (5e5, 2.0, 163840), (1e4, 0.5, 5000), (1e7, 64.0, 524288)]:
+        zhi = AW.window_zhi_from_kret(H.D, base, k_ret, 1 << 20)
+        w = WR.wavelengths_sorted(H.D, base, k_ret)
+        n_pages = -(-N // 16)
+        got = ops.decode_page_levels(n_pages, N, zhi, dev).cpu()
+        segs = WR.deff_segments("decode", 0, N, 1, 16, N, w, H.D)
+        exp = []
+        for n0, n1, deff in segs:
+            exp += [deff // 16] * (-(-(n1 - n0) // 16))
+        assert got.tolist() == exp, (base, k_ret, N)
+
+
+def test_hnd_layout_and_strided_q(dev):
+    from atflash import interface
+    g = torch.Generator().manual_seed(8)
+    N, hq, hkv = 777, 24, 8
+    q = H.randn_bf16((hq, H.D), g)
+    k = H.randn_bf16((N, hkv, H.D), g)
+    v = H.randn_bf16((N, hkv, H.D), g)
+    a = interface.single_decode_with_kv_cache(q.to(dev), k.to(dev), v.to(dev), kv_layout="NHD")
+    b = interface.single_decode_with_kv_cache(q.to(dev), k.transpose(0, 1).contiguous().to(dev),
+                                              v.transpose(0, 1).contiguous().to(dev), kv_layout="HND")
+    assert torch.equal(a.cpu(), b.cpu())

@@ -1,0 +1,64 @@
+"""Paged KV-cache writer: layout bit-exact against a CPU indexing model, RoPE
+within one bf16 rounding of the fp32 oracle rotation (GPU)."""
+import pytest
+import torch
+
+import helpers as H
+
+pytestmark = pytest.mark.gpu
+
+
+def _expected_pages(k, v, table, start, n_pages_pool, hkv, layout=0):
+    """CPU model of the cache layout for one sequence (no RoPE)."""
+    P = 64
+    ek = torch.zeros((n_pages_pool, hkv, 8, 16, 16), dtype=torch.bfloat16)
+    ev = torch.zeros((n_pages_pool, hkv, 128, 16), dtype=torch.bfloat16)
+    slot_of = [4 * [0, 2, 1, 3][t // 4] + t % 4 for t in range(16)]
+    for t in range(k.shape[0]):
+        pos = start + t
+        pg = table[pos // 16]
+        s = pos % 16
+        for lv in range(8):
+            c0 = P - 8 * (lv + 1) if layout == 0 else 16 * lv
+            c1 = c0 + P if layout == 0 else 16 * lv + 8
+            ek[pg, :, lv, s, :8] = k[t, :, c0:c0 + 8]
+            ek[pg, :, lv, s, 8:] = k[t, :, c1:c1 + 8]
+        ev[pg, :, :, slot_of[s]] = v[t]
+    return ek, ev
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+def test_cache_layout_bit_exact(layout, dev):
+    g = torch.Generator().manual_seed(4)
+    hkv, n, start, pool = 4, 203, 37, 40
+    k = H.randn_bf16((n, hkv, H.D), g)
+    v = H.randn_bf16((n, hkv, H.D), g)
+    table = torch.randperm(pool, generator=g)[:-(-(start + n) // 16)].to(torch.int32)
+    kc = torch.zeros((pool, hkv, 8, 16, 16), dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros((pool, hkv, 128, 16), dtype=torch.bfloat16, device=dev)
+    torch.ops.atflash.kv_write(kc, vc, k[None].to(dev), v[None].to(dev),
+                               torch.tensor([start], dtype=torch.int32, device=dev),
+                               table[None].to(dev).contiguous(), None, layout)
+    ek, ev = _expected_pages(k, v, table.tolist(), start, pool, hkv, layout)
+    assert torch.equal(kc.cpu(), ek)
+    assert torch.equal(vc.cpu(), ev)
+
+
+def test_rope_at_write_matches_fp32_rotation(dev):
+    from atflash import rope as R
+    g = torch.Generator().manual_seed(6)
+    hkv, n, base = 2, 300, 1e7
+    k = H.randn_bf16((n, hkv, H.D), g)
+    v = H.randn_bf16((n, hkv, H.D), g)
+    table = torch.arange(-(-n // 16), dtype=torch.int32)
+    kc = torch.zeros((len(table), hkv, 8, 16, 16), dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros((len(table), hkv, 128, 16), dtype=torch.bfloat16, device=dev)
+    rt = R.rope_table(n, R.inv_freq(H.D, base, dev))
+    torch.ops.atflash.kv_write(kc, vc, k[None].to(dev), v[None].to(dev),
+                               torch.zeros(1, dtype=torch.int32, device=dev), table[None].to(dev), rt, 0)
+    kr = H.rotate(k[None], torch.arange(n), base)[0]       # fp32 oracle rotation
+    ek, _ = _expected_pages(kr, v, table.tolist(), 0, len(table), hkv)  # cast to bf16 inside
+    got = kc.cpu().float()
+    want = ek.float()
+    # one bf16 rounding of a value of magnitude |x| (<= ~6): 2^-8 relative
+    assert ((got - want).abs() <= want.abs() * 2 ** -7 + 1e-6).all()
