@@ -138,7 +138,8 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(PrefillArgs a) {
 
   // ---- prologue: stage tile 0 ----
   if (t_end_wg > 0) {
-    const int L0 = levels_of(a.lt, max(0, pos0_wg - (kPfTileN * 0 + 31)));
+    // levels of the nearest key of the tile for the workgroup's first row
+    const int L0 = levels_of(a.lt, max(0, pos0_wg - (kPfTileN - 1)));
     pf_load_tile(a, b, kvh, 0, L0, smem, wave, lane);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -164,7 +165,7 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(PrefillArgs a) {
     }
     // Prefetch tile t+1 into the other stage.
     if (t + 1 < t_end_wg) {
-      const int L1 = levels_of(a.lt, max(0, pos0_wg - ((t + 1) * kPfTileN + 31)));
+      const int L1 = levels_of(a.lt, max(0, pos0_wg - ((t + 1) * kPfTileN + kPfTileN - 1)));
       pf_load_tile(a, b, kvh, t + 1, L1, smem + ((t + 1) & 1) * kPfStageBytes, wave, lane);
     }
 

@@ -3,6 +3,7 @@ within one bf16 rounding of the fp32 oracle rotation (GPU)."""
 import pytest
 import torch
 
+import atflash.ops  # noqa: F401  (registers torch.ops.atflash)
 import helpers as H
 
 pytestmark = pytest.mark.gpu
