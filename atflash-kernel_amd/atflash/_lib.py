@@ -26,7 +26,7 @@ LEVELS = 8
 PAGE_SIZE = 16
 LAYOUT_HALF_SPLIT = 0
 LAYOUT_SORTED_PAIR = 1
-PREFILL_BLOCK_M = 64
+PREFILL_BLOCK_M = 32
 PREFILL_BLOCK_N = 32
 DECODE_BLOCK_N = 16
 MAX_GQA_GROUP = 16

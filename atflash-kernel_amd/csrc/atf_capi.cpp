@@ -61,12 +61,14 @@ int check_layout(int layout, const float* rope_cs, int rope_max_pos) {
 
 void decode_split(int batch, int hkv, int max_seq_len, int* n_splits, int* pages_per_split) {
   const int pages = max_seq_len > 0 ? (max_seq_len + atf::kPage - 1) / atf::kPage : 1;
-  const int target_waves = 1024;
+  // ~2 waves per SIMD over 256 CUs, at least 8 pages (two 4-page groups) per split
+  const int target_waves = 2048;
   int ns = (target_waves + batch * hkv - 1) / (batch * hkv);
   if (ns < 1) ns = 1;
   if (ns > pages) ns = pages;
   int pps = (pages + ns - 1) / ns;
   if (pps < 8) pps = pages < 8 ? pages : 8;
+  if ((pages + pps - 1) / pps > atf::kDecMaxSplits) pps = (pages + atf::kDecMaxSplits - 1) / atf::kDecMaxSplits;
   *pages_per_split = pps;
   *n_splits = (pages + pps - 1) / pps;
 }

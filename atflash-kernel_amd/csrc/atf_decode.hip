@@ -195,26 +195,58 @@ __global__ __launch_bounds__(64) void decode_split_kernel(DecodeArgs a) {
   }
 }
 
-// One workgroup per (q head, sequence), one thread per output dim.
-__global__ __launch_bounds__(128) void decode_merge_kernel(MergeArgs a) {
+// One workgroup of 256 threads per (q head, sequence).  The split weights
+// w_s = exp2((m_s - M) c) go to LDS once; the weighted sum over splits is then
+// read as coalesced 128-float rows, two splits in flight per thread pair.
+__device__ __forceinline__ float block_reduce(float v, float* red, bool is_max) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float o = __shfl_xor(v, off);
+    v = is_max ? fmaxf(v, o) : v + o;
+  }
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  v = red[0];
+#pragma unroll
+  for (int i = 1; i < 4; ++i) v = is_max ? fmaxf(v, red[i]) : v + red[i];
+  return v;
+}
+
+__global__ __launch_bounds__(256) void decode_merge_kernel(MergeArgs a) {
+  __shared__ float wsh[kDecMaxSplits];
+  __shared__ float red[4];
+  __shared__ float half_acc[kD];
   const int qh = blockIdx.x, b = blockIdx.y;
-  const int d = threadIdx.x;
+  const int tid = threadIdx.x;
   const int h = qh / a.group, g = qh % a.group;
   const int64_t base = (static_cast<int64_t>(b) * a.hkv + h) * a.n_splits;
-  float M = -__builtin_huge_valf();
-  for (int s = 0; s < a.n_splits; ++s) M = fmaxf(M, a.ws_ml[((base + s) * kDecMaxGroup + g) * 2]);
-  float L = 0.f, acc = 0.f;
-  if (M != -__builtin_huge_valf()) {
-    for (int s = 0; s < a.n_splits; ++s) {
-      const int64_t pi = (base + s) * kDecMaxGroup + g;
-      const float m = a.ws_ml[pi * 2];
-      const float w = fast_exp2((m - M) * a.scale_log2);  // m = -inf -> 0
-      L += w * a.ws_ml[pi * 2 + 1];
-      acc += w * a.ws_o[pi * kD + d];
-    }
+  const float NEG_INF = -__builtin_huge_valf();
+  float M = NEG_INF;
+  for (int s = tid; s < a.n_splits; s += 256) M = fmaxf(M, a.ws_ml[((base + s) * kDecMaxGroup + g) * 2]);
+  M = block_reduce(M, red, true);
+  float L = 0.f;
+  for (int s = tid; s < a.n_splits; s += 256) {
+    const int64_t pi = (base + s) * kDecMaxGroup + g;
+    const float m = a.ws_ml[pi * 2];
+    const float w = (M == NEG_INF) ? 0.f : fast_exp2((m - M) * a.scale_log2);  // m = -inf -> 0
+    wsh[s] = w;
+    L += w * a.ws_ml[pi * 2 + 1];
   }
-  const float o = L > 0.f ? acc / L : 0.f;
-  a.out[static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(qh) * a.o_sh + d] = f32_to_bf16(o);
+  L = block_reduce(L, red, false);  // also orders the wsh writes before the reads below
+  const int d = tid & (kD - 1);
+  const int part = tid >> 7;
+  float acc = 0.f;
+#pragma unroll 8
+  for (int s = part; s < a.n_splits; s += 2) acc += wsh[s] * a.ws_o[((base + s) * kDecMaxGroup + g) * kD + d];
+  if (part == 1) half_acc[d] = acc;
+  __syncthreads();
+  if (part == 0) {
+    acc += half_acc[d];
+    const float o = L > 0.f ? acc / L : 0.f;
+    a.out[static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(qh) * a.o_sh + d] = f32_to_bf16(o);
+  }
 }
 
 // Level count per page for one sequence of length N (decode rule, block_n = 16).
@@ -229,7 +261,7 @@ hipError_t launch_decode(const DecodeArgs& a, const MergeArgs& m, hipStream_t s)
   hipLaunchKernelGGL(decode_split_kernel, dim3(a.n_splits, a.hkv, a.batch), dim3(64), 0, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(decode_merge_kernel, dim3(m.hq, m.batch), dim3(kD), 0, s, m);
+  hipLaunchKernelGGL(decode_merge_kernel, dim3(m.hq, m.batch), dim3(256), 0, s, m);
   return hipGetLastError();
 }
 

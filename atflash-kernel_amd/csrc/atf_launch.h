@@ -5,9 +5,11 @@
 namespace atf {
 
 // Prefill geometry (the oracle's tile quantization is block_m = kPfRowsWave
-// query positions by block_n = kPfWinN keys).
-constexpr int kPfWaves = 4;
-constexpr int kPfRowsWave = 64;
+// query positions by block_n = kPfWinN keys).  8 waves of 32 rows: at most 256
+// registers per wave, so two waves share each SIMD and one wave's softmax
+// overlaps the other's MFMAs.
+constexpr int kPfWaves = 8;
+constexpr int kPfRowsWave = 32;
 constexpr int kPfRowsWg = kPfWaves * kPfRowsWave;
 constexpr int kPfTileN = 64;
 constexpr int kPfWinN = 32;
@@ -17,6 +19,7 @@ constexpr int kPfLdsBytes = 2 * kPfStageBytes;
 // Decode geometry (block_n = one page).
 constexpr int kDecMaxGroup = 16;
 constexpr int kDecUnroll = 4;
+constexpr int kDecMaxSplits = 1024;
 
 struct KvWriteArgs {
   uint16_t* k_cache;

@@ -5,22 +5,27 @@
 // microbench/b1_correctness.py:84-85, e2e_pipeline/atflash_e2e_fafi.py:118-119).
 //
 // Work decomposition
-//   workgroup = 4 waves = 256 consecutive query positions of one q head;
-//   wave      = 64 positions = two 32-row MFMA blocks ("rb");
+//   workgroup = 8 waves = 256 consecutive query positions of one q head;
+//   wave      = 32 positions (one MFMA row block); two waves share each SIMD, so
+//               the softmax VALU work of one overlaps the MFMAs of the other;
 //   k-tile    = 64 keys = 4 cache pages, staged through LDS (double buffered) with
 //               direct global->LDS loads; the window is quantized per 32-key block
-//               ("kb"), i.e. the oracle tile is (block_m, block_n) = (64, 32).
+//               ("kb"), i.e. the oracle tile is (block_m, block_n) = (32, 32).
 //   S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_32x32x16_bf16: the accumulator
 //   lane l always holds query row l%32, so the online-softmax max/sum stay in the
 //   lane except one exchange with lane l^32 (v_permlane32_swap).
 //   Per (wave, kb) the QK contraction runs over the first L = D_eff/16 levels
 //   only, and the workgroup copies only the levels its first wave needs, so the
 //   out-of-window K levels never enter LDS.  Q is rotated (RoPE) at load.
+//   Online softmax with a lazily updated reference max: O and l are rescaled only
+//   when a row's max grows by more than 2^8 in exp2 units, so P <= 256.
 #include "atf_launch.h"
 
 namespace atf {
 
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
+
+constexpr float kLazyRescaleLog2 = 8.0f;
 
 __device__ __forceinline__ float pair_max(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -31,44 +36,74 @@ __device__ __forceinline__ float pair_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// Stage one 64-key tile (4 pages) of K (first L levels) and V into LDS.
-// Wave w copies page w of the tile.
+// acc + x.lo + x.hi for a packed bf16 pair (row sums of the bf16 P used in PV).
+// Written as the VOP3P instruction: the clang builtin for the bf16 dot2 lowers
+// to the VOP2 form with the same source register for every element of a
+// vector (ROCm 7.2), which sums the wrong values.
+__device__ __forceinline__ float dot2_ones(uint32_t x, float acc) {
+  asm("v_dot2_f32_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(x), "v"(0x3f803f80u));
+  return acc;
+}
+
+__device__ __forceinline__ bf16x8 lds_frag(const lds_u8* p) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) bf16x8*>(p);
+}
+
+// Stage one 64-key tile (4 pages) into LDS: waves 0-3 copy K (first L levels)
+// of page w, waves 4-7 copy V of page w-4.  Missing pages are zero-filled.
 __device__ __forceinline__ void pf_load_tile(const PrefillArgs& a, int b, int kvh, int t, int L,
                                              lds_u8* stage, int wave, int lane) {
-  const int pidx = 4 * t + wave;
+  const int page = wave & 3;
+  const bool is_v = wave >= 4;
+  const int pidx = 4 * t + page;
   const int n_pages_k = (a.nk + kPage - 1) / kPage;
   int pg = -1;
   if (pidx < n_pages_k) {
     pg = a.page_table[static_cast<int64_t>(b) * a.max_pages + pidx];
     if (pg < 0 || pg >= a.num_pages) pg = -1;
   }
-  lds_u8* kdst = stage + wave * 4096;
-  lds_u8* vdst = stage + 4 * 4096 + wave * 4096;
+  lds_u8* dst = stage + (is_v ? 4 * 4096 : 0) + page * 4096;
   if (pg < 0) {
     const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(kdst + i * 1024 + lane * 16) = z;
-      *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(vdst + i * 1024 + lane * 16) = z;
-    }
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(dst + i * 1024 + lane * 16) = z;
     return;
   }
   const size_t blk = (static_cast<size_t>(pg) * a.hkv + kvh) * 4096;
-  const uint8_t* ksrc = reinterpret_cast<const uint8_t*>(a.k_cache) + blk;
-  const uint8_t* vsrc = reinterpret_cast<const uint8_t*>(a.v_cache) + blk;
-  const int npairs = (L + 1) >> 1;
-  for (int lp = 0; lp < npairs; ++lp) {
-    if (lane < 32 || 2 * lp + 1 < L) {
-      __builtin_amdgcn_global_load_lds(ksrc + lp * 1024 + lane * 16, kdst + lp * 1024, 16, 0, 0);
-    }
-  }
+  if (is_v) {
+    const uint8_t* src = reinterpret_cast<const uint8_t*>(a.v_cache) + blk;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    __builtin_amdgcn_global_load_lds(vsrc + i * 1024 + lane * 16, vdst + i * 1024, 16, 0, 0);
+    for (int i = 0; i < 4; ++i) __builtin_amdgcn_global_load_lds(src + i * 1024 + lane * 16, dst + i * 1024, 16, 0, 0);
+  } else {
+    const uint8_t* src = reinterpret_cast<const uint8_t*>(a.k_cache) + blk;
+    const int npairs = (L + 1) >> 1;
+    for (int lp = 0; lp < npairs; ++lp) {
+      if (lane < 32 || 2 * lp + 1 < L)
+        __builtin_amdgcn_global_load_lds(src + lp * 1024 + lane * 16, dst + lp * 1024, 16, 0, 0);
+    }
   }
 }
 
-__global__ __launch_bounds__(256, 1) void prefill_kernel(PrefillArgs a) {
+// S^T (32 keys x 32 rows) over the first L levels, highest level first.
+__device__ __forceinline__ f32x16 qk_levels(const bf16x8 (&kf)[kLevels], const u32x4 (&Qf)[kLevels], int L) {
+  f32x16 S = f32x16{};
+#define ATF_QK(l) S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[l], __builtin_bit_cast(bf16x8, Qf[l]), S, 0, 0, 0)
+  switch (L) {
+    case 8: ATF_QK(7); [[fallthrough]];
+    case 7: ATF_QK(6); [[fallthrough]];
+    case 6: ATF_QK(5); [[fallthrough]];
+    case 5: ATF_QK(4); [[fallthrough]];
+    case 4: ATF_QK(3); [[fallthrough]];
+    case 3: ATF_QK(2); [[fallthrough]];
+    case 2: ATF_QK(1); [[fallthrough]];
+    default: ATF_QK(0);
+  }
+#undef ATF_QK
+  return S;
+}
+
+__global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
   lds_u8* smem = (lds_u8*)(smem_raw);
 
@@ -98,14 +133,14 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(PrefillArgs a) {
   const int n_ktiles = (a.nk + kPfTileN - 1) / kPfTileN;
   const int last_wg = a.q_offset + min(a.nq, lr0_wg + kPfRowsWg) - 1;
   const int t_end_wg = min(n_ktiles, last_wg / kPfTileN + 1);
-  const int t_end = (lr0 < a.nq) ? min(n_ktiles, (a.q_offset + min(a.nq, lr0 + kPfRowsWave) - 1) / kPfTileN + 1) : 0;
+  const int t_end =
+      (lr0 < a.nq) ? min(n_ktiles, (a.q_offset + min(a.nq, lr0 + kPfRowsWave) - 1) / kPfTileN + 1) : 0;
 
   // ---- Q fragments (B operand of S^T = K Q^T), RoPE applied at load ----
-  u32x4 Qf[2][kLevels];
+  u32x4 Qf[kLevels];
   const bool second = lane >= 32;
-#pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const int row = lr0 + rb * 32 + (lane & 31);
+  const int row = lr0 + (lane & 31);
+  {
     const uint16_t* qrow = a.q + static_cast<int64_t>(b) * a.q_sb + static_cast<int64_t>(row) * a.q_st +
                            static_cast<int64_t>(h) * a.q_sh;
 #pragma unroll
@@ -122,26 +157,20 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(PrefillArgs a) {
           v = ldg16(qrow + (second ? c1 : c0));
         }
       }
-      Qf[rb][l] = v;
+      Qf[l] = v;
     }
   }
 
-  f32x16 O[2][4];
+  f32x16 O[4];
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-    for (int db = 0; db < 4; ++db) O[rb][db] = f32x16{};
+  for (int db = 0; db < 4; ++db) O[db] = f32x16{};
   const float NEG_INF = -__builtin_huge_valf();
-  float m_run[2] = {NEG_INF, NEG_INF};
-  float l_run[2] = {0.f, 0.f};
+  float m_ref = NEG_INF;  // reference max of the exponentials (raw score units)
+  float l_run = 0.f;      // this lane's partial row sum relative to m_ref
   const float c = a.scale_log2;
 
-  // ---- prologue: stage tile 0 ----
-  if (t_end_wg > 0) {
-    // levels of the nearest key of the tile for the workgroup's first row
-    const int L0 = levels_of(a.lt, max(0, pos0_wg - (kPfTileN - 1)));
-    pf_load_tile(a, b, kvh, 0, L0, smem, wave, lane);
-  }
+  // ---- prologue: stage tile 0 (levels of its nearest key for the first row) ----
+  if (t_end_wg > 0) pf_load_tile(a, b, kvh, 0, levels_of(a.lt, max(0, pos0_wg - (kPfTileN - 1))), smem, wave, lane);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
@@ -150,114 +179,83 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(PrefillArgs a) {
     const int n0 = t * kPfTileN;
     // Keys past nk in the last tile: zero their V so that 0 * V stays 0.
     if (n0 + kPfTileN > a.nk) {
-      const int page = threadIdx.x >> 6;
-      const int row2 = (threadIdx.x & 63) * 2;
+      const int page = threadIdx.x >> 7;
+      __attribute__((address_space(3))) uint16_t* vrow = reinterpret_cast<__attribute__((address_space(3))) uint16_t*>(
+          cur + 4 * 4096 + page * 4096 + (threadIdx.x & 127) * 32);
 #pragma unroll
-      for (int rr = 0; rr < 2; ++rr) {
-        __attribute__((address_space(3))) uint16_t* vrow =
-            reinterpret_cast<__attribute__((address_space(3))) uint16_t*>(cur + 4 * 4096 + page * 4096 +
-                                                                          (row2 + rr) * 32);
-#pragma unroll
-        for (int tk = 0; tk < kPage; ++tk)
-          if (n0 + page * kPage + tk >= a.nk) vrow[v_slot(tk)] = 0;
-      }
+      for (int tk = 0; tk < kPage; ++tk)
+        if (n0 + page * kPage + tk >= a.nk) vrow[v_slot(tk)] = 0;
       __syncthreads();
     }
-    // Prefetch tile t+1 into the other stage.
     if (t + 1 < t_end_wg) {
       const int L1 = levels_of(a.lt, max(0, pos0_wg - ((t + 1) * kPfTileN + kPfTileN - 1)));
       pf_load_tile(a, b, kvh, t + 1, L1, smem + ((t + 1) & 1) * kPfStageBytes, wave, lane);
     }
 
     if (t < t_end) {
-      int Lk[2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) Lk[kb] = levels_of(a.lt, max(0, pos0 - (n0 + 32 * kb + 31)));
-
-      // ---- S^T = K Q^T over the surviving levels ----
-      f32x16 S[2][2];
+      // ---- S^T = K Q^T over the surviving levels of each 32-key block ----
+      f32x16 S[2];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        S[0][kb] = f32x16{};
-        S[1][kb] = f32x16{};
+        const int L = levels_of(a.lt, max(0, pos0 - (n0 + 32 * kb + 31)));
         const lds_u8* kbase = cur + (2 * kb + ((lane & 31) >> 4)) * 4096 + (lane & 15) * 32 + (lane >> 5) * 16;
+        bf16x8 kf[kLevels];
 #pragma unroll
-        for (int l = 0; l < kLevels; ++l) {
-          if (l < Lk[kb]) {
-            const bf16x8 kf = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8*>(kbase + l * 512);
-            S[0][kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, __builtin_bit_cast(bf16x8, Qf[0][l]), S[0][kb], 0, 0, 0);
-            S[1][kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, __builtin_bit_cast(bf16x8, Qf[1][l]), S[1][kb], 0, 0, 0);
-          }
-        }
+        for (int l = 0; l < kLevels; ++l) kf[l] = lds_frag(kbase + l * 512);  // unread levels stay unused
+        S[kb] = qk_levels(kf, Qf, L);
       }
 
       // ---- online softmax (lane = query row) ----
       const bool need_mask = (n0 + kPfTileN - 1 > pos0) || (n0 + kPfTileN > a.nk);
-      bf16x8 Pf[2][4];
+      const int row_pos = pos0 + (lane & 31);
+      float mx = NEG_INF;
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
-        const int row_pos = pos0 + rb * 32 + (lane & 31);
-        float mx = NEG_INF;
+      for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            float s = S[rb][kb][r];
-            if (need_mask) {
-              const int key = n0 + 32 * kb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-              if (key > row_pos || key >= a.nk) s = NEG_INF;
-            }
-            S[rb][kb][r] = s;
-            mx = fmaxf(mx, s);
+        for (int r = 0; r < 16; ++r) {
+          if (need_mask) {
+            const int key = n0 + 32 * kb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            if (key > row_pos || key >= a.nk) S[kb][r] = NEG_INF;
           }
+          mx = fmaxf(mx, S[kb][r]);
         }
-        mx = pair_max(mx);
-        const float m_new = fmaxf(m_run[rb], mx);
-        float alpha, msc;
-        if (m_new == NEG_INF) {
-          alpha = 1.f;
-          msc = 0.f;
-        } else {
-          alpha = fast_exp2((m_run[rb] - m_new) * c);
-          msc = m_new * c;
-        }
-        m_run[rb] = m_new;
-        float ls = 0.f;
+      }
+      mx = pair_max(mx);
+      const bool grow = mx * c > m_ref * c + kLazyRescaleLog2;
+      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+        const float alpha = grow ? fast_exp2((m_ref - mx) * c) : 1.f;  // m_ref = -inf -> 0
+        if (grow) m_ref = mx;
+        l_run *= alpha;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
+        for (int db = 0; db < 4; ++db) O[db] *= alpha;
+      }
+      const float msc = (m_ref == NEG_INF) ? 0.f : m_ref * c;
+      bf16x8 Pf[4];
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float p = fast_exp2(__builtin_fmaf(S[rb][kb][r], c, -msc));
-            S[rb][kb][r] = p;
-            ls += p;
+      for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int hs = 0; hs < 2; ++hs) {
+          u32x4 pk;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float p0 = fast_exp2(__builtin_fmaf(S[kb][8 * hs + 2 * i], c, -msc));
+            const float p1 = fast_exp2(__builtin_fmaf(S[kb][8 * hs + 2 * i + 1], c, -msc));
+            pk[i] = pack_bf16x2(p0, p1);
+            l_run = dot2_ones(pk[i], l_run);
           }
-        }
-        l_run[rb] = l_run[rb] * alpha + ls;
-#pragma unroll
-        for (int db = 0; db < 4; ++db) O[rb][db] *= alpha;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-          for (int hs = 0; hs < 2; ++hs) {
-            u32x4 pk;
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              pk[i] = pack_bf16x2(S[rb][kb][8 * hs + 2 * i], S[rb][kb][8 * hs + 2 * i + 1]);
-            Pf[rb][2 * kb + hs] = __builtin_bit_cast(bf16x8, pk);
-          }
+          Pf[2 * kb + hs] = __builtin_bit_cast(bf16x8, pk);
         }
       }
 
       // ---- O^T += V^T P^T ----
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
+        bf16x8 vf[4];
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const bf16x8 vf = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8*>(
-              cur + 4 * 4096 + ks * 4096 + (32 * db + (lane & 31)) * 32 + (lane >> 5) * 16);
-          O[0][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, Pf[0][ks], O[0][db], 0, 0, 0);
-          O[1][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, Pf[1][ks], O[1][db], 0, 0, 0);
-        }
+        for (int ks = 0; ks < 4; ++ks)
+          vf[ks] = lds_frag(cur + 4 * 4096 + ks * 4096 + (32 * db + (lane & 31)) * 32 + (lane >> 5) * 16);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) O[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[ks], Pf[ks], O[db], 0, 0, 0);
       }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -265,35 +263,31 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(PrefillArgs a) {
   }
 
   // ---- epilogue: normalise and store ----
+  const float l = pair_sum(l_run);
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  if (row < a.nq) {
+    uint16_t* orow = a.out + static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(row) * a.o_st +
+                     static_cast<int64_t>(h) * a.o_sh;
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const float l = pair_sum(l_run[rb]);
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    const int row = lr0 + rb * 32 + (lane & 31);
-    if (row < a.nq) {
-      uint16_t* orow = a.out + static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(row) * a.o_st +
-                       static_cast<int64_t>(h) * a.o_sh;
+    for (int db = 0; db < 4; ++db) {
 #pragma unroll
-      for (int db = 0; db < 4; ++db) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int d = 32 * db + 8 * g + 4 * (lane >> 5);
-          u32x2 w;
-          w[0] = pack_bf16x2(O[rb][db][4 * g + 0] * inv, O[rb][db][4 * g + 1] * inv);
-          w[1] = pack_bf16x2(O[rb][db][4 * g + 2] * inv, O[rb][db][4 * g + 3] * inv);
-          *reinterpret_cast<u32x2*>(orow + d) = w;
-        }
+      for (int g = 0; g < 4; ++g) {
+        const int d = 32 * db + 8 * g + 4 * (lane >> 5);
+        u32x2 w;
+        w[0] = pack_bf16x2(O[db][4 * g + 0] * inv, O[db][4 * g + 1] * inv);
+        w[1] = pack_bf16x2(O[db][4 * g + 2] * inv, O[db][4 * g + 3] * inv);
+        *reinterpret_cast<u32x2*>(orow + d) = w;
       }
-      if (a.lse != nullptr && lane < 32) {
-        a.lse[(static_cast<int64_t>(b) * a.hq + h) * a.nq + row] =
-            (l > 0.f) ? m_run[rb] * a.sm_scale + __logf(l) : NEG_INF;
-      }
+    }
+    if (a.lse != nullptr && lane < 32) {
+      a.lse[(static_cast<int64_t>(b) * a.hq + h) * a.nq + row] =
+          (l > 0.f) ? m_ref * a.sm_scale + __logf(l) : NEG_INF;
     }
   }
 }
 
-// Level count per (64-row wave tile, 32-key block), from the same device rule
-// the kernel uses; out is [n_row_tiles][n_kblocks].
+// Level count per (32-row tile, 32-key block), from the same device rule the
+// kernel uses; out is [n_row_tiles][n_kblocks].
 __global__ void prefill_tile_levels_kernel(int32_t* out, int n_row_tiles, int n_kblocks, int q_offset,
                                            LevelTable lt) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;

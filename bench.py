@@ -18,10 +18,10 @@ stream, with device synchronisation around the timed region.
 configuration's numbers are in `detail`.
 roofline  prefill attention kernel (MFMA bound): algorithmic FLOPs per launch
           (2*Hq*N^2*d window OFF; Hq*N^2*d*(1+s) window ON, s = QK slice ratio
-          at the kernel's (64, 32) tiles) / mean kernel time, against 2.5 PFLOP/s;
+          at the kernel's (32, 32) tiles) / mean kernel time, against 2.5 PFLOP/s;
           the decode kernel pair (HBM bound) is in `roofline_decode`.
 cpu_baseline  the oracle's fp32 banded reference (oracle/attention.py) on the
-          host cores, on a sample of 64-row query tiles of the same 128K prefill,
+          host cores, on a sample of 32-row query tiles of the same 128K prefill,
           extrapolated to the whole prefill (cost is linear in the tile position).
 """
 import argparse
@@ -133,15 +133,15 @@ def slice_ratios(N):
     out = {}
     for name, k_ret in (("k2", 2.0), ("k64", 64.0)):
         zhi = AW.window_zhi_from_kret(D, BASE, k_ret, 1 << 23)
-        st = AW.slice_stats("prefill", N, N, 64, 32, zhi, D)
+        st = AW.slice_stats("prefill", N, N, 32, 32, zhi, D)
         s_dec, _ = FW.decode_s(N, zhi, D, 16)
         out[name] = {"s_prefill": st["qk_slice_ratio"], "s_decode": s_dec}
     return out
 
 
-def cpu_baseline(N, samples=4):
-    """The oracle on host cores for `samples` 64-row tiles spread over the 128K
-    prefill (window k = 2), extrapolated to all N/64 tiles."""
+def cpu_baseline(N, samples=48):
+    """The oracle on host cores for `samples` 32-row tiles spread over the 128K
+    prefill (window k = 2), extrapolated to all N/32 tiles."""
     import torch
     from oracle import attention as OA
     from oracle import window_rule as WR
@@ -149,22 +149,22 @@ def cpu_baseline(N, samples=4):
     torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(0)
     w = WR.wavelengths_sorted(D, BASE, 2.0)
-    rows = [int(((i + 0.5) / samples) * N) // 64 * 64 for i in range(samples)]
-    hi = max(rows) + 64
+    rows = [int(((i + 0.5) / samples) * N) // 32 * 32 for i in range(samples)]
+    hi = max(rows) + 32
     q = torch.randn((1, HQ, N, D), generator=g)
     k = torch.randn((1, HKV, hi, D), generator=g)
     v = torch.randn((1, HKV, hi, D), generator=g)
     def run(tiles):
         t0 = time.perf_counter()
-        OA.ref_window_attn(q[:, :, :hi], k, v, w, phase="prefill", block_m=64, block_n=32, tile_rows=tiles)
+        OA.ref_window_attn(q[:, :, :hi], k, v, w, phase="prefill", block_m=32, block_n=32, tile_rows=tiles)
         return time.perf_counter() - t0
     fixed = run([])            # per-call work independent of the tiles (GQA expand, casts)
     sampled = run(rows)
     per_tile = max(0.0, sampled - fixed) / samples
-    est_s = fixed * (N / hi) + per_tile * (N / 64)
+    est_s = fixed * (N / hi) + per_tile * (N / 32)
     return {"value": est_s * 1e3, "unit": "ms", "cores": threads, "kind": "port",
-            "sample": f"oracle fp32 ref_window_attn (window k=2, tiles 64x32) on {samples} 64-row query tiles at "
-                      f"rows {rows} of the {N}-token Qwen2.5-7B-shape prefill; mean tile time x {N // 64} tiles "
+            "sample": f"oracle fp32 ref_window_attn (window k=2, tiles 32x32) on {samples} 32-row query tiles at "
+                      f"rows {rows} of the {N}-token Qwen2.5-7B-shape prefill; mean tile time x {N // 32} tiles "
                       f"+ the per-call GQA expand scaled to N; CPU seconds measured {fixed + sampled:.1f}",
             "per_tile_s": per_tile, "fixed_s": fixed}
 

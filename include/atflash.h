@@ -44,7 +44,7 @@ extern "C" {
 #define ATF_LAYOUT_HALF_SPLIT 0
 #define ATF_LAYOUT_SORTED_PAIR 1
 /* Tile quantization of the window (the block_m/block_n the oracle must use). */
-#define ATF_PREFILL_BLOCK_M 64
+#define ATF_PREFILL_BLOCK_M 32
 #define ATF_PREFILL_BLOCK_N 32
 #define ATF_DECODE_BLOCK_N 16
 #define ATF_MAX_GQA_GROUP 16
@@ -122,7 +122,7 @@ int atf_decode_paged_bf16(void* out, int64_t o_sb, int64_t o_sh,
 /*
  * Per-tile level counts (D_eff / 16) as the kernels compute them, for tests of
  * the integer window path.  prefill: out int32 [n_row_tiles][n_kblocks] for
- * 64-row query tiles starting at q_offset + 64*i and 32-key blocks;
+ * 32-row query tiles starting at q_offset + 32*i and 32-key blocks;
  * decode: out int32 [n_pages] for a sequence of length seq_len.
  * Mirror atflash/window_table.py deff_segments (79-102) at these tiles.
  */

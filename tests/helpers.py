@@ -10,7 +10,7 @@ D = 128
 BF = torch.bfloat16
 TOL_MAX = 2e-2   # max |out - fp32 oracle|
 TOL_MEAN = 1e-3  # mean |out - fp32 oracle|
-PREFILL_BM, PREFILL_BN, DECODE_BN = 64, 32, 16
+PREFILL_BM, PREFILL_BN, DECODE_BN = 32, 32, 16
 
 
 def randn_bf16(shape, gen):
@@ -38,7 +38,7 @@ def rotate(x_bshd, positions, base):
 
 def prefill_oracle(q, k, v, base, k_ret, rope, q_offset=0, tile_rows=None, mode="fp32"):
     """fp32 oracle of the prefill kernel: optional RoPE (fp32), sorted-pair layout,
-    tiles (64, 32).  q [B, Nq, Hq, D] and k, v [B, Nk, Hkv, D] bf16, half-split."""
+    tiles (32, 32).  q [B, Nq, Hq, D] and k, v [B, Nk, Hkv, D] bf16, half-split."""
     Nq, Nk = q.shape[1], k.shape[1]
     if rope:
         qr = rotate(q, torch.arange(q_offset, q_offset + Nq), base)

@@ -61,5 +61,10 @@ def test_rope_at_write_matches_fp32_rotation(dev):
     ek, _ = _expected_pages(kr, v, table.tolist(), 0, len(table), hkv)  # cast to bf16 inside
     got = kc.cpu().float()
     want = ek.float()
-    # one bf16 rounding of a value of magnitude |x| (<= ~6): 2^-8 relative
-    assert ((got - want).abs() <= want.abs() * 2 ** -7 + 1e-6).all()
+    # one bf16 rounding (2^-8 relative, allow 2^-7) plus an absolute floor for
+    # rotated values that cancel to ~0, where the GPU and CPU cos/sin (each
+    # correctly rounded fp32, but computed differently) can differ by an ulp
+    err = (got - want).abs()
+    assert (err <= torch.maximum(want.abs(), got.abs()) * 2 ** -7 + 1e-4).all(), err.max()
+    # a wrong pair, sign or position would be O(1) off
+    assert err.max().item() < 0.05

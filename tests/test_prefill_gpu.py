@@ -118,29 +118,29 @@ def test_chunked_equals_single_shot_bitwise(k_ret, dev):
 
 
 def test_tile_levels_match_oracle_segments(dev):
-    """Per-(64-row, 32-key) tile level counts computed on the GPU equal
+    """Per-(32-row, 32-key) tile level counts computed on the GPU equal
     D_eff/16 from the oracle's deff_segments."""
     from atflash import atflash_window as AW, ops
     for base, k_ret, N, q_off in [(1e7, 2.0, 8192, 0), (5e5, 2.0, 4096, 1024), (1e4, 0.5, 2048, 64)]:
         zhi = AW.window_zhi_from_kret(H.D, base, k_ret, 1 << 20)
         w = WR.wavelengths_sorted(H.D, base, k_ret)
-        nrt = (N - q_off) // 64
+        nrt = (N - q_off) // 32
         nkb = N // 32
         got = ops.prefill_tile_levels(nrt, nkb, q_off, zhi, dev).cpu()
         for rt in range(0, nrt, 7):
-            q0 = q_off + 64 * rt
-            segs = WR.deff_segments("prefill", q0, min(q0 + 64, N), 64, 32, N, w, H.D)
+            q0 = q_off + 32 * rt
+            segs = WR.deff_segments("prefill", q0, min(q0 + 32, N), 32, 32, N, w, H.D)
             for n0, n1, deff in segs:
                 for kb in range(n0 // 32, -(-n1 // 32)):
                     assert got[rt, kb].item() * 16 == deff, (base, rt, kb)
 
 
 def test_long_context_sampled_rows(dev):
-    """Qwen2.5-7B shape at N = 16K, k = 2: sampled 64-row tiles against the oracle."""
+    """Qwen2.5-7B shape at N = 16K, k = 2: sampled 32-row tiles against the oracle."""
     base, N, hq, hkv = 1e7, 16384, 28, 4
     q, k, v = H.qkv(1, N, hq, hkv, seed=21)
     out, _ = _run(q, k, v, base, 2.0, True, dev)
-    rows = [0, 64 * 37, 64 * 130, N - 64]
+    rows = [0, 32 * 37, 32 * 130, N - 32]
     ref = H.prefill_oracle(q, k, v, base, 2.0, True, tile_rows=rows)
     for r in rows:
-        H.assert_close(out[:, r:r + 64], ref[:, r:r + 64], f"rows {r}")
+        H.assert_close(out[:, r:r + 32], ref[:, r:r + 32], f"rows {r}")
