@@ -6,9 +6,12 @@
 //
 // Work decomposition
 //   workgroup = 8 waves = 256 consecutive query positions of one q head;
-//   wave      = 32 positions (one MFMA row block); two waves share each SIMD, so
-//               the softmax VALU work of one overlaps the MFMAs of the other;
-//   k-tile    = 64 keys = 4 cache pages, staged through LDS (double buffered) with
+//   wave      = 32 positions (one MFMA row block).  Waves w and w+4 share a SIMD
+//               and run one phase apart ("ping-pong"): at every step one of them
+//               issues MFMAs (PV of tile t-1, then QK of tile t) while the other
+//               runs the softmax of its current tile, so the matrix pipe and the
+//               VALU work at the same time;
+//   k-tile    = 64 keys = 4 cache pages, staged through a 3-deep LDS ring with
 //               direct global->LDS loads; the window is quantized per 32-key block
 //               ("kb"), i.e. the oracle tile is (block_m, block_n) = (32, 32).
 //   S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_32x32x16_bf16: the accumulator
@@ -44,6 +47,32 @@ __device__ __forceinline__ float dot2_ones(uint32_t x, float acc) {
   asm("v_dot2_f32_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(x), "v"(0x3f803f80u));
   return acc;
 }
+
+// Level count of tile t for a fixed (query anchor, key offset) pair as t walks
+// up: level i is read from tile T_i = ceil((anchor - off - zhi[i]) / 64) on, so
+// L(t) = #{i : T_i <= t} (the D_eff rule at distance anchor - (64 t + off)).
+// advance(t) costs one compare per tile except when a level boundary is crossed.
+struct LevelWalker {
+  int L;
+  int next;
+  int anchor;
+  __device__ __forceinline__ int start_tile(const LevelTable& lt, int i) const {
+    const int z = min(lt.zhi[i], 1 << 30);
+    return (anchor - z + kPfTileN - 1) >> 6;  // ceil((anchor - zhi) / 64), arithmetic shift
+  }
+  __device__ __forceinline__ void init(const LevelTable& lt, int anchor_minus_off) {
+    anchor = anchor_minus_off;
+    L = 0;
+    next = start_tile(lt, 0);
+  }
+  __device__ __forceinline__ int advance(const LevelTable& lt, int t) {
+    while (t >= next) {
+      ++L;
+      next = (L < kLevels) ? start_tile(lt, L) : 0x7fffffff;
+    }
+    return L < 1 ? 1 : L;  // D_eff >= 16
+  }
+};
 
 __device__ __forceinline__ bf16x8 lds_frag(const lds_u8* p) {
   return *reinterpret_cast<const __attribute__((address_space(3))) bf16x8*>(p);
@@ -85,22 +114,77 @@ __device__ __forceinline__ void pf_load_tile(const PrefillArgs& a, int b, int kv
   }
 }
 
-// S^T (32 keys x 32 rows) over the first L levels, highest level first.
-__device__ __forceinline__ f32x16 qk_levels(const bf16x8 (&kf)[kLevels], const u32x4 (&Qf)[kLevels], int L) {
+// S^T (32 keys x 32 rows) of one 32-key block over its first L levels: one MFMA
+// chain, the operand of level l+1 read from LDS while level l's MFMA runs.  `a`
+// holds the level-0 operand on entry.
+template <int L>
+__device__ __forceinline__ f32x16 qk_chain(const lds_u8* kbase, const u32x4 (&Qf)[kLevels], bf16x8 a) {
   f32x16 S = f32x16{};
-#define ATF_QK(l) S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[l], __builtin_bit_cast(bf16x8, Qf[l]), S, 0, 0, 0)
-  switch (L) {
-    case 8: ATF_QK(7); [[fallthrough]];
-    case 7: ATF_QK(6); [[fallthrough]];
-    case 6: ATF_QK(5); [[fallthrough]];
-    case 5: ATF_QK(4); [[fallthrough]];
-    case 4: ATF_QK(3); [[fallthrough]];
-    case 3: ATF_QK(2); [[fallthrough]];
-    case 2: ATF_QK(1); [[fallthrough]];
-    default: ATF_QK(0);
+#pragma unroll
+  for (int l = 0; l < L; ++l) {
+    bf16x8 an = a;
+    if (l + 1 < L) an = lds_frag(kbase + (l + 1) * 512);
+    S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, __builtin_bit_cast(bf16x8, Qf[l]), S, 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    a = an;
   }
-#undef ATF_QK
   return S;
+}
+
+// Both 32-key blocks with the same level count: two interleaved chains,
+// operands one level ahead.
+template <int L>
+__device__ __forceinline__ void qk_pair(const lds_u8* k0, const lds_u8* k1, const u32x4 (&Qf)[kLevels], bf16x8 a,
+                                        bf16x8 b, f32x16& S0, f32x16& S1) {
+  S0 = f32x16{};
+  S1 = f32x16{};
+#pragma unroll
+  for (int l = 0; l < L; ++l) {
+    bf16x8 an = a, bn = b;
+    if (l + 1 < L) {
+      an = lds_frag(k0 + (l + 1) * 512);
+      bn = lds_frag(k1 + (l + 1) * 512);
+    }
+    S0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, __builtin_bit_cast(bf16x8, Qf[l]), S0, 0, 0, 0);
+    S1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, __builtin_bit_cast(bf16x8, Qf[l]), S1, 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    a = an;
+    b = bn;
+  }
+}
+
+__device__ __forceinline__ f32x16 qk_one(int L, const lds_u8* kbase, const u32x4 (&Qf)[kLevels], bf16x8 a) {
+  switch (L) {
+    case 8: return qk_chain<8>(kbase, Qf, a);
+    case 7: return qk_chain<7>(kbase, Qf, a);
+    case 6: return qk_chain<6>(kbase, Qf, a);
+    case 5: return qk_chain<5>(kbase, Qf, a);
+    case 4: return qk_chain<4>(kbase, Qf, a);
+    case 3: return qk_chain<3>(kbase, Qf, a);
+    case 2: return qk_chain<2>(kbase, Qf, a);
+    default: return qk_chain<1>(kbase, Qf, a);
+  }
+}
+
+// S^T for the two 32-key blocks of a tile with level counts L0 (far) and L1
+// (near); a0/a1 hold their level-0 operands.
+__device__ __forceinline__ void qk_tile(int L0, int L1, const lds_u8* k0, const lds_u8* k1,
+                                        const u32x4 (&Qf)[kLevels], bf16x8 a0, bf16x8 a1, f32x16& S0, f32x16& S1) {
+  if (L0 == L1) {
+    switch (L0) {
+      case 8: qk_pair<8>(k0, k1, Qf, a0, a1, S0, S1); break;
+      case 7: qk_pair<7>(k0, k1, Qf, a0, a1, S0, S1); break;
+      case 6: qk_pair<6>(k0, k1, Qf, a0, a1, S0, S1); break;
+      case 5: qk_pair<5>(k0, k1, Qf, a0, a1, S0, S1); break;
+      case 4: qk_pair<4>(k0, k1, Qf, a0, a1, S0, S1); break;
+      case 3: qk_pair<3>(k0, k1, Qf, a0, a1, S0, S1); break;
+      case 2: qk_pair<2>(k0, k1, Qf, a0, a1, S0, S1); break;
+      default: qk_pair<1>(k0, k1, Qf, a0, a1, S0, S1); break;
+    }
+  } else {
+    S0 = qk_one(L0, k0, Qf, a0);
+    S1 = qk_one(L1, k1, Qf, a1);
+  }
 }
 
 __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a) {
@@ -168,44 +252,96 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
   float m_ref = NEG_INF;  // reference max of the exponentials (raw score units)
   float l_run = 0.f;      // this lane's partial row sum relative to m_ref
   const float c = a.scale_log2;
+  const int T = t_end_wg;
+#ifndef ATF_PF_GROUP
+#define ATF_PF_GROUP(w) ((w) >> 2)
+#define ATF_PF_RANK(w) ((w) & 3)
+#endif
+  const int grp = ATF_PF_GROUP(wave);  // ping-pong group (waves w and w+4 share a SIMD)
+  const int rank = ATF_PF_RANK(wave);  // 0..3 within the group
 
-  // ---- prologue: stage tile 0 (levels of its nearest key for the first row) ----
-  if (t_end_wg > 0) pf_load_tile(a, b, kvh, 0, levels_of(a.lt, max(0, pos0_wg - (kPfTileN - 1))), smem, wave, lane);
+  // Level walkers: far (keys n0..n0+31) and near (n0+32..n0+63) blocks of this
+  // wave, and the workgroup's staging count (nearest key, first row).
+  LevelWalker w_far, w_near, w_ld;
+  w_far.init(a.lt, pos0 - 31);
+  w_near.init(a.lt, pos0 - 63);
+  w_ld.init(a.lt, pos0_wg - 63);
+
+  // LDS ring: byte offsets of the stages holding tiles t-1, t and t+1.
+  int o_prev = 2 * kPfStageBytes, o_cur = 0, o_next = kPfStageBytes;
+
+  // ---- prologue: stage tile 0 ----
+  if (T > 0) pf_load_tile(a, b, kvh, 0, w_ld.advance(a.lt, 0), smem + o_cur, wave, lane);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
+  if (T > 0 && kPfTileN > a.nk) {  // zero V of keys past nk (0 * V must stay 0)
+    const int page = threadIdx.x >> 7;
+    __attribute__((address_space(3))) uint16_t* vrow = reinterpret_cast<__attribute__((address_space(3))) uint16_t*>(
+        smem + o_cur + 4 * 4096 + page * 4096 + (threadIdx.x & 127) * 32);
+#pragma unroll
+    for (int tk = 0; tk < kPage; ++tk)
+      if (page * kPage + tk >= a.nk) vrow[v_slot(tk)] = 0;
+    __syncthreads();
+  }
 
-  for (int t = 0; t < t_end_wg; ++t) {
-    lds_u8* cur = smem + (t & 1) * kPfStageBytes;
-    const int n0 = t * kPfTileN;
-    // Keys past nk in the last tile: zero their V so that 0 * V stays 0.
-    if (n0 + kPfTileN > a.nk) {
-      const int page = threadIdx.x >> 7;
-      __attribute__((address_space(3))) uint16_t* vrow = reinterpret_cast<__attribute__((address_space(3))) uint16_t*>(
-          cur + 4 * 4096 + page * 4096 + (threadIdx.x & 127) * 32);
+  f32x16 S[2];
+  bf16x8 Pf[4];
 #pragma unroll
-      for (int tk = 0; tk < kPage; ++tk)
-        if (n0 + page * kPage + tk >= a.nk) vrow[v_slot(tk)] = 0;
-      __syncthreads();
-    }
-    if (t + 1 < t_end_wg) {
-      const int L1 = levels_of(a.lt, max(0, pos0_wg - ((t + 1) * kPfTileN + kPfTileN - 1)));
-      pf_load_tile(a, b, kvh, t + 1, L1, smem + ((t + 1) & 1) * kPfStageBytes, wave, lane);
-    }
-
-    if (t < t_end) {
-      // ---- S^T = K Q^T over the surviving levels of each 32-key block ----
-      f32x16 S[2];
+  for (int i = 0; i < 4; ++i) Pf[i] = bf16x8{};
+  // Global step k: group g runs phase k - g.  Phase 2t is the MFMA phase of
+  // tile t (PV of tile t-1, QK of tile t), phase 2t+1 its softmax.  Tile t+1 is
+  // requested at step 2t and has landed after the barrier ending step 2t+1
+  // (group 0: end of its softmax of t; group 1: end of its MFMA phase of t).
+  // The MFMA phase runs unconditionally (P = 0 when there is nothing to add) so
+  // the accumulators stay in place.
+  if (grp == 1) {
+    if (1 < T) pf_load_tile(a, b, kvh, 1, w_ld.advance(a.lt, 1), smem + o_next, wave, lane);
+    __syncthreads();  // group 1 starts one step late
+  }
+  for (int t = 0; t <= T; ++t) {
+    if (grp == 0 && t + 1 < T) pf_load_tile(a, b, kvh, t + 1, w_ld.advance(a.lt, t + 1), smem + o_next, wave, lane);
+    // ---- MFMA phase of tile t ----
+#ifndef ATF_PF_NO_PRIO
+    __builtin_amdgcn_s_setprio(1);
+#endif
+    {
+      const lds_u8* kbase = smem + o_cur + ((lane & 31) >> 4) * 4096 + (lane & 15) * 32 + (lane >> 5) * 16;
+      // O^T += V^T P^T for tile t-1 (P = 0 at t = 0); the operands of step ks+1
+      // (and finally the level-0 K operands of tile t) are read while step ks runs.
+      const lds_u8* vb = smem + (t == 0 ? o_cur : o_prev) + 4 * 4096 + (lane & 31) * 32 + (lane >> 5) * 16;
+      bf16x8 vf[4], vn[4], a0, a1;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const int L = levels_of(a.lt, max(0, pos0 - (n0 + 32 * kb + 31)));
-        const lds_u8* kbase = cur + (2 * kb + ((lane & 31) >> 4)) * 4096 + (lane & 15) * 32 + (lane >> 5) * 16;
-        bf16x8 kf[kLevels];
+      for (int db = 0; db < 4; ++db) vf[db] = lds_frag(vb + db * 1024);
 #pragma unroll
-        for (int l = 0; l < kLevels; ++l) kf[l] = lds_frag(kbase + l * 512);  // unread levels stay unused
-        S[kb] = qk_levels(kf, Qf, L);
+      for (int ks = 0; ks < 4; ++ks) {
+        if (ks < 3) {
+#pragma unroll
+          for (int db = 0; db < 4; ++db) vn[db] = lds_frag(vb + (ks + 1) * 4096 + db * 1024);
+        } else {
+          a0 = lds_frag(kbase);
+          a1 = lds_frag(kbase + 2 * 4096);
+        }
+#pragma unroll
+        for (int db = 0; db < 4; ++db) O[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db], Pf[ks], O[db], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int db = 0; db < 4; ++db) vf[db] = vn[db];
       }
-
-      // ---- online softmax (lane = query row) ----
+      // S^T = K Q^T over the surviving levels of each 32-key block of tile t
+      // (unused when the wave has no tile t).
+      const int L0 = w_far.advance(a.lt, t);
+      const int L1 = w_near.advance(a.lt, t);
+      qk_tile(L0, L1, kbase, kbase + 2 * 4096, Qf, a0, a1, S[0], S[1]);
+    }
+#ifndef ATF_PF_NO_PRIO
+    __builtin_amdgcn_s_setprio(0);
+#endif
+    if (grp == 1) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (grp == 1 && t + 2 < T) pf_load_tile(a, b, kvh, t + 2, w_ld.advance(a.lt, t + 2), smem + o_prev, wave, lane);
+    // ---- softmax phase of tile t (lane = query row) ----
+    if (t < t_end) {
+      const int n0 = t * kPfTileN;
       const bool need_mask = (n0 + kPfTileN - 1 > pos0) || (n0 + kPfTileN > a.nk);
       const int row_pos = pos0 + (lane & 31);
       float mx = NEG_INF;
@@ -230,7 +366,6 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
         for (int db = 0; db < 4; ++db) O[db] *= alpha;
       }
       const float msc = (m_ref == NEG_INF) ? 0.f : m_ref * c;
-      bf16x8 Pf[4];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
@@ -246,21 +381,32 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
           Pf[2 * kb + hs] = __builtin_bit_cast(bf16x8, pk);
         }
       }
-
-      // ---- O^T += V^T P^T ----
+    } else {
 #pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        bf16x8 vf[4];
+      for (int i = 0; i < 4; ++i) Pf[i] = bf16x8{};
+    }
+    if (grp == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    // Tile t+1 has landed; group 0 zeroes the V of keys past nk in a partial
+    // last tile (read no earlier than two barriers later).
+    if (grp == 0 && t + 1 < T && (t + 1) * kPfTileN + kPfTileN > a.nk) {
+      const int n0 = (t + 1) * kPfTileN;
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-          vf[ks] = lds_frag(cur + 4 * 4096 + ks * 4096 + (32 * db + (lane & 31)) * 32 + (lane >> 5) * 16);
+      for (int rr = 0; rr < 2; ++rr) {
+        __attribute__((address_space(3))) uint16_t* vrow = reinterpret_cast<__attribute__((address_space(3))) uint16_t*>(
+            smem + o_next + 4 * 4096 + rank * 4096 + (lane * 2 + rr) * 32);
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) O[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[ks], Pf[ks], O[db], 0, 0, 0);
+        for (int tk = 0; tk < kPage; ++tk)
+          if (n0 + rank * kPage + tk >= a.nk) vrow[v_slot(tk)] = 0;
       }
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+    // rotate the ring: tile t+1 becomes current
+    const int o_old = o_prev;
+    o_prev = o_cur;
+    o_cur = o_next;
+    o_next = o_old;
   }
+  if (grp == 0) __syncthreads();  // group 0 ends one step late
 
   // ---- epilogue: normalise and store ----
   const float l = pair_sum(l_run);
@@ -286,15 +432,18 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
   }
 }
 
-// Level count per (32-row tile, 32-key block), from the same device rule the
-// kernel uses; out is [n_row_tiles][n_kblocks].
+// Level count per (32-row tile, 32-key block) through the LevelWalker the
+// attention kernel uses (even blocks are the far half of a 64-key tile, odd
+// blocks the near half); out is [n_row_tiles][n_kblocks].
 __global__ void prefill_tile_levels_kernel(int32_t* out, int n_row_tiles, int n_kblocks, int q_offset,
                                            LevelTable lt) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n_row_tiles * n_kblocks) return;
   const int rt = i / n_kblocks, kb = i % n_kblocks;
   const int pos0 = q_offset + rt * kPfRowsWave;
-  out[i] = levels_of(lt, max(0, pos0 - (32 * kb + 31)));
+  LevelWalker w;
+  w.init(lt, pos0 - ((kb & 1) ? 63 : 31));
+  out[i] = w.advance(lt, kb >> 1);
 }
 
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t s) {
