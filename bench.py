@@ -78,7 +78,7 @@ def bench_gpu(args):
     res = {"prefill": {}, "prefill_attn": {}, "decode": {}}
 
     # ---- prefill: full op ----
-    for name, zhi in windows.items():
+    for name, zhi in (windows.items() if args.only in ("all", "prefill") else []):
         fn = lambda: interface._flash_attn_fwd(q, k, v, atflash_window_zhi=zhi, rope=rt)  # noqa: E731
         for _ in range(args.warmup):
             fn()
@@ -87,7 +87,7 @@ def bench_gpu(args):
 
     # ---- prefill attention kernel alone (roofline), on a pre-packed cache ----
     kc, vc, table = interface.pack_kv(k, v, rope=rt)
-    for name, zhi in windows.items():
+    for name, zhi in (windows.items() if args.only in ("all", "prefill") else []):
         zl = None if zhi is None else list(zhi)
         fn = lambda: ops.prefill(q, kc, vc, table, N, 0, zl, scale, rt, 0)  # noqa: E731
         for _ in range(max(1, args.warmup // 2)):
@@ -112,7 +112,7 @@ def bench_gpu(args):
     seq = torch.tensor([N], dtype=torch.int32, device=dev)
     del q, k, v
     torch.cuda.empty_cache()
-    for name, zhi in windows.items():
+    for name, zhi in (windows.items() if args.only in ("all", "decode") else []):
         zl = None if zhi is None else list(zhi)
         it = [0]
 
@@ -176,6 +176,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--n", type=int, default=131072)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", choices=("all", "prefill", "decode", "copy"), default="all",
+                    help="run one workload (for profiler runs); 'copy' is a plain 1 GiB device copy "
+                         "used to calibrate the FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (see DESIGN.md, sharding).",
@@ -191,9 +194,19 @@ def main():
         __graft_entry__.build()
 
     N = args.n
+    if args.only == "copy":
+        src = torch.ones(1 << 29, dtype=torch.bfloat16, device="cuda")  # 1 GiB
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": src.numel() * 2}))
+        return
     torch.cuda.synchronize()
     t_wall = time.perf_counter()
     res = bench_gpu(args)
+    if args.only != "all":
+        print(json.dumps({"only": args.only, "stats": res}))
+        return
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_wall
     sr = slice_ratios(N)
