@@ -115,6 +115,22 @@ def _(q, k_cache, v_cache, page_table, nk, q_offset, zhi, sm_scale, rope_cs, lay
     return q.new_empty((B, Nq, Hq, D)), q.new_empty((B, Hq, Nq), dtype=torch.float32)
 
 
+# Decode workspaces, one per (device, stream): zero-filled when allocated, and
+# every completed decode call leaves its arrival counters at zero again.  Calls
+# on one stream are ordered, so they can share a workspace.
+_DECODE_WS = {}
+
+
+def _decode_workspace(device, nbytes):
+    stream = torch.cuda.current_stream(device)
+    key = (device.index, stream.cuda_stream)
+    ws = _DECODE_WS.get(key)
+    if ws is None or ws.numel() * 4 < nbytes:
+        ws = torch.zeros((max(nbytes, 16) + 3) // 4, dtype=torch.float32, device=device)
+        _DECODE_WS[key] = ws
+    return ws
+
+
 @torch.library.custom_op("atflash::decode_paged", mutates_args=())
 def decode_paged(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, page_table: torch.Tensor,
                  seq_lens: torch.Tensor, max_seq_len: int, zhi: Optional[List[int]], sm_scale: float,
@@ -134,7 +150,7 @@ def decode_paged(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
     rope_cs, max_pos = _rope(rope_cs)
     L = _lib.lib()
     nbytes = int(L.atf_decode_workspace_bytes(B, Hq, hkv, int(max_seq_len)))
-    ws = torch.empty((max(nbytes, 16) + 3) // 4, dtype=torch.float32, device=q.device)
+    ws = _decode_workspace(q.device, nbytes)
     out = torch.empty((B, Hq, _lib.HEAD_DIM), dtype=torch.bfloat16, device=q.device)
     _lib.check(L.atf_decode_paged_bf16(
         _lib.ptr(out), out.stride(0), out.stride(1), _lib.ptr(q), q.stride(0), q.stride(1),
@@ -150,7 +166,7 @@ def _(q, k_cache, v_cache, page_table, seq_lens, max_seq_len, zhi, sm_scale, rop
 
 
 def prefill_tile_levels(n_row_tiles: int, n_kblocks: int, q_offset: int, zhi, device="cuda") -> torch.Tensor:
-    """Level counts the prefill kernel uses per (64-row tile, 32-key block)."""
+    """Level counts the prefill kernel uses per (32-row tile, 32-key block)."""
     out = torch.empty((n_row_tiles, n_kblocks), dtype=torch.int32, device=device)
     _lib.check(_lib.lib().atf_prefill_tile_levels(_lib.ptr(out), n_row_tiles, n_kblocks, q_offset,
                                                   _lib.zhi_array(zhi), _lib.stream_of(out.device)))

@@ -61,16 +61,22 @@ int check_layout(int layout, const float* rope_cs, int rope_max_pos) {
 
 void decode_split(int batch, int hkv, int max_seq_len, int* n_splits, int* pages_per_split) {
   const int pages = max_seq_len > 0 ? (max_seq_len + atf::kPage - 1) / atf::kPage : 1;
-  // ~2 waves per SIMD over 256 CUs, at least 8 pages (two 4-page groups) per split
-  const int target_waves = 2048;
-  int ns = (target_waves + batch * hkv - 1) / (batch * hkv);
+  // one workgroup (8 waves) per CU over 256 CUs; at least one 4-page group per wave
+  const int target_wgs = 256;
+  const int min_pps = atf::kDecUnroll * atf::kDecWaves;
+  int ns = (target_wgs + batch * hkv - 1) / (batch * hkv);
   if (ns < 1) ns = 1;
-  if (ns > pages) ns = pages;
   int pps = (pages + ns - 1) / ns;
-  if (pps < 8) pps = pages < 8 ? pages : 8;
+  if (pps < min_pps) pps = min_pps;
   if ((pages + pps - 1) / pps > atf::kDecMaxSplits) pps = (pages + atf::kDecMaxSplits - 1) / atf::kDecMaxSplits;
   *pages_per_split = pps;
   *n_splits = (pages + pps - 1) / pps;
+}
+
+// Workspace: [counters: B*Hkv uint32, padded to kDecCounterBytes][ws_ml][ws_o].
+size_t counter_bytes(int batch, int hkv) {
+  const size_t c = static_cast<size_t>(batch) * hkv * sizeof(uint32_t);
+  return (c + atf::kDecCounterBytes - 1) / atf::kDecCounterBytes * atf::kDecCounterBytes;
 }
 
 }  // namespace
@@ -179,7 +185,8 @@ size_t atf_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, 
   if (batch <= 0 || num_kv_heads <= 0) return 0;
   int ns = 1, pps = 1;
   decode_split(batch, num_kv_heads, max_seq_len, &ns, &pps);
-  return static_cast<size_t>(batch) * num_kv_heads * ns * atf::kDecMaxGroup * (atf::kD + 2) * sizeof(float);
+  return counter_bytes(batch, num_kv_heads) +
+         static_cast<size_t>(batch) * num_kv_heads * ns * atf::kDecMaxGroup * (atf::kD + 2) * sizeof(float);
 }
 
 int atf_decode_paged_bf16(void* out, int64_t o_sb, int64_t o_sh, const void* q, int64_t q_sb, int64_t q_sh,
@@ -203,9 +210,10 @@ int atf_decode_paged_bf16(void* out, int64_t o_sb, int64_t o_sh, const void* q, 
   if (int r = check_layout(layout, rope_cs, rope_max_pos)) return r;
   if (rope_cs && max_seq_len > rope_max_pos)
     return fail(ATF_ERR_INVALID, "rope table has %d positions, need %d", rope_max_pos, max_seq_len);
-  if (!aligned(q, 16) || !aligned(out, 2) || !aligned(k_cache, 16) || !aligned(v_cache, 16))
-    return fail(ATF_ERR_INVALID, "q and caches must be 16-byte aligned");
+  if (!aligned(q, 16) || !aligned(out, 8) || !aligned(k_cache, 16) || !aligned(v_cache, 16))
+    return fail(ATF_ERR_INVALID, "q, caches must be 16-byte and out 8-byte aligned");
   if (q_sb % 8 || q_sh % 8) return fail(ATF_ERR_INVALID, "q strides must be multiples of 8 elements");
+  if (o_sb % 4 || o_sh % 4) return fail(ATF_ERR_INVALID, "out strides must be multiples of 4 elements");
   const size_t need = atf_decode_workspace_bytes(batch, num_q_heads, num_kv_heads, max_seq_len);
   if (!workspace || workspace_bytes < need || !aligned(workspace, 16))
     return fail(ATF_ERR_WORKSPACE, "workspace of %zu bytes (16-byte aligned) required, got %zu", need,
@@ -233,22 +241,14 @@ int atf_decode_paged_bf16(void* out, int64_t o_sb, int64_t o_sh, const void* q, 
   a.scale_log2 = sm_scale * 1.4426950408889634f;
   a.rope_cs = rope_cs;
   a.layout = layout;
-  float* ws = static_cast<float*>(workspace);
-  a.ws_o = ws;
-  a.ws_ml = ws + static_cast<size_t>(batch) * num_kv_heads * ns * atf::kDecMaxGroup * atf::kD;
-  atf::MergeArgs m{};
-  m.out = static_cast<uint16_t*>(out);
-  m.o_sb = o_sb;
-  m.o_sh = o_sh;
-  m.ws_o = a.ws_o;
-  m.ws_ml = a.ws_ml;
-  m.batch = batch;
-  m.hq = num_q_heads;
-  m.hkv = num_kv_heads;
-  m.group = a.group;
-  m.n_splits = ns;
-  m.scale_log2 = a.scale_log2;
-  hipError_t e = atf::launch_decode(a, m, static_cast<hipStream_t>(stream));
+  a.out = static_cast<uint16_t*>(out);
+  a.o_sb = o_sb;
+  a.o_sh = o_sh;
+  char* ws = static_cast<char*>(workspace);
+  a.counters = reinterpret_cast<uint32_t*>(ws);
+  a.ws_ml = reinterpret_cast<float*>(ws + counter_bytes(batch, num_kv_heads));
+  a.ws_o = a.ws_ml + static_cast<size_t>(batch) * num_kv_heads * ns * atf::kDecMaxGroup * 2;
+  hipError_t e = atf::launch_decode(a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "decode launch");
   return ok();
 }

@@ -5,16 +5,21 @@
 // kernels/flashinfer_port/fiwin_common.py:96-112, e2e_pipeline/atflash_e2e_fafi.py:106-109;
 // window predicate: kernels/flashinfer_port/decode.cuh.diff:47-89).
 //
-// One wave per (sequence, kv head, split of pages).  The G = Hq/Hkv query heads
-// of the kv head are the 16 columns of v_mfma_f32_16x16x32_bf16 (S^T = K Q^T,
-// two 16-dim levels per instruction) and v_mfma_f32_16x16x16_bf16
-// (O^T = V^T P^T, 16 tokens per instruction).  K and V are loaded straight into
-// the MFMA operand registers (no LDS).  The window predicate is per page:
-// page p is read for its first L(p) = D_eff/16 levels, where
-// D_eff = 16 * #{i : zhi[i] >= (N-1) - (16p+15)}; the loads of the other levels
-// are never issued, so out-of-window K bytes are not read from HBM.  Each split
-// writes an unnormalised partial (m, l, o); a second kernel merges the partials
-// by log-sum-exp.
+// One workgroup of 8 waves per (sequence, kv head, split of pages); each wave
+// streams its own pages.  The G = Hq/Hkv query heads of the kv head are the 16
+// columns of v_mfma_f32_16x16x32_bf16 (S^T = K Q^T, two 16-dim levels per
+// instruction) and v_mfma_f32_16x16x16_bf16 (O^T = V^T P^T, 16 tokens per
+// instruction).  K and V are loaded straight into the MFMA operand registers.
+// The window predicate is per page: page p is read for its first
+// L(p) = D_eff/16 levels, D_eff = 16 * #{i : zhi[i] >= (N-1) - (16p+15)}; the
+// loads of the other levels are never issued, so out-of-window K bytes are not
+// read from HBM.
+//
+// Merging, all in the one launch: the 8 wave partials (m, l, o) of a split are
+// combined in LDS and written to the workspace; the last workgroup to finish
+// for a (sequence, kv head) -- it sees the device-scope arrival counter reach
+// n_splits - 1 -- merges the split partials by log-sum-exp, writes the output
+// and resets the counter to zero for the next call.
 #include "atf_launch.h"
 
 namespace atf {
@@ -70,9 +75,20 @@ __device__ __forceinline__ void dec_load_page(const DecodeArgs& a, int b, int h,
   }
 }
 
-__global__ __launch_bounds__(64) void decode_split_kernel(DecodeArgs a) {
+// two waves per SIMD: at most 256 registers per wave
+__global__ __launch_bounds__(kDecWaves * 64) __attribute__((amdgpu_waves_per_eu(2)))
+void decode_kernel(DecodeArgs a) {
+  // wave partials; in the merging workgroup, afterwards, the split weights
+  __shared__ __attribute__((aligned(16))) float sh_o[kDecWaves * kDecMaxGroup * kD];
+  __shared__ float sh_m[kDecWaves * kDecMaxGroup], sh_l[kDecWaves * kDecMaxGroup];
+  __shared__ float red[kDecWaves * 64];
+  __shared__ float sh_M[kDecMaxGroup], sh_L[kDecMaxGroup];
+  __shared__ int sh_last;
+  static_assert(kDecMaxSplits * kDecMaxGroup <= kDecWaves * kDecMaxGroup * kD, "split weights must fit sh_o");
+
   const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
   const int g = lane & 15;
   const int N = max(0, min(a.seq_lens[b], a.max_seq_len));
   const int n_pages = (N + kPage - 1) / kPage;
@@ -112,7 +128,8 @@ __global__ __launch_bounds__(64) void decode_split_kernel(DecodeArgs a) {
   for (int db = 0; db < 8; ++db) O[db] = f32x4{};
   float m_run = NEG_INF, l_run = 0.f;
 
-  for (int p0 = p_begin; p0 < p_end; p0 += kDecUnroll) {
+  // wave w takes the groups of kDecUnroll pages that start at p_begin + kDecUnroll * (w + kDecWaves * i)
+  for (int p0 = p_begin + kDecUnroll * wave; p0 < p_end; p0 += kDecUnroll * kDecWaves) {
     PageRegs pr[kDecUnroll];
 #pragma unroll
     for (int u = 0; u < kDecUnroll; ++u) {
@@ -179,74 +196,133 @@ __global__ __launch_bounds__(64) void decode_split_kernel(DecodeArgs a) {
     }
   }
 
+  // ---- the split's partial: combine the wave partials in LDS ----
   const float l_tot = quad_sum(l_run);
-  const int64_t part = ((static_cast<int64_t>(b) * a.hkv + h) * a.n_splits + s) * kDecMaxGroup;
   if (g < a.group) {
-    float* o = a.ws_o + (part + g) * kD;
 #pragma unroll
     for (int db = 0; db < 8; ++db) {
       const int d = 16 * db + 4 * (lane >> 4);
-      *reinterpret_cast<f32x4*>(o + d) = O[db];
+      *reinterpret_cast<f32x4*>(&sh_o[(wave * kDecMaxGroup + g) * kD + d]) = O[db];
     }
     if (lane < 16) {
-      a.ws_ml[(part + g) * 2 + 0] = m_run;
-      a.ws_ml[(part + g) * 2 + 1] = l_tot;
+      sh_m[wave * kDecMaxGroup + g] = m_run;
+      sh_l[wave * kDecMaxGroup + g] = l_tot;
     }
   }
-}
-
-// One workgroup of 256 threads per (q head, sequence).  The split weights
-// w_s = exp2((m_s - M) c) go to LDS once; the weighted sum over splits is then
-// read as coalesced 128-float rows, two splits in flight per thread pair.
-__device__ __forceinline__ float block_reduce(float v, float* red, bool is_max) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __syncthreads();
+  // thread t owns query head t / 32, dims 4 (t % 32) .. +3 (group <= 16: 512 tasks)
+  const int gq = tid >> 5, d4 = 4 * (tid & 31);
+  const bool owner = gq < a.group;
+  const int64_t pbase = (static_cast<int64_t>(b) * a.hkv + h) * a.n_splits * kDecMaxGroup;  // split 0, head 0
+  if (owner) {
+    float M = NEG_INF;
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const float o = __shfl_xor(v, off);
-    v = is_max ? fmaxf(v, o) : v + o;
+    for (int w = 0; w < kDecWaves; ++w) M = fmaxf(M, sh_m[w * kDecMaxGroup + gq]);
+    float L = 0.f;
+    f32x4 acc = f32x4{};
+    if (M != NEG_INF) {
+#pragma unroll
+      for (int w = 0; w < kDecWaves; ++w) {
+        const float wt = fast_exp2((sh_m[w * kDecMaxGroup + gq] - M) * c);  // empty wave: m = -inf -> 0
+        L += wt * sh_l[w * kDecMaxGroup + gq];
+        acc += wt * *reinterpret_cast<const f32x4*>(&sh_o[(w * kDecMaxGroup + gq) * kD + d4]);
+      }
+    }
+    const int64_t pi = pbase + static_cast<int64_t>(s) * kDecMaxGroup + gq;
+    *reinterpret_cast<f32x4*>(a.ws_o + pi * kD + d4) = acc;
+    if (d4 == 0) {
+      a.ws_ml[pi * 2 + 0] = M;
+      a.ws_ml[pi * 2 + 1] = L;
+    }
+  }
+
+  // ---- arrival: the last split of (b, h) to finish merges all splits ----
+  // One release per workgroup: the barrier orders every wave's partial stores
+  // before thread 0's agent-scope release increment (each device-scope fence
+  // writes back the XCD's L2, so it is issued once, not per wave).
+  __syncthreads();
+  uint32_t* cnt = a.counters + (static_cast<int64_t>(b) * a.hkv + h);
+  if (tid == 0) {
+    const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = (old == static_cast<uint32_t>(a.n_splits - 1)) ? 1 : 0;
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // the other splits' partials are visible
+    sh_last = last;
   }
   __syncthreads();
-  if (lane == 0) red[w] = v;
-  __syncthreads();
-  v = red[0];
-#pragma unroll
-  for (int i = 1; i < 4; ++i) v = is_max ? fmaxf(v, red[i]) : v + red[i];
-  return v;
-}
+  if (!sh_last) return;
 
-__global__ __launch_bounds__(256) void decode_merge_kernel(MergeArgs a) {
-  __shared__ float wsh[kDecMaxSplits];
-  __shared__ float red[4];
-  __shared__ float half_acc[kD];
-  const int qh = blockIdx.x, b = blockIdx.y;
-  const int tid = threadIdx.x;
-  const int h = qh / a.group, g = qh % a.group;
-  const int64_t base = (static_cast<int64_t>(b) * a.hkv + h) * a.n_splits;
-  const float NEG_INF = -__builtin_huge_valf();
+  // split weights w_s = exp2((m_s - M) c) and L = sum_s w_s l_s per query head;
+  // thread (gi, part) holds the (m, l) of splits part, part + 32, ... in registers
+  constexpr int kParts = kDecWaves * 64 / kDecMaxGroup;
+  constexpr int kPerPart = (kDecMaxSplits + kParts - 1) / kParts;
+  const int gi = tid & (kDecMaxGroup - 1), part = tid >> 4;
+  float ml[kPerPart][2];
   float M = NEG_INF;
-  for (int s = tid; s < a.n_splits; s += 256) M = fmaxf(M, a.ws_ml[((base + s) * kDecMaxGroup + g) * 2]);
-  M = block_reduce(M, red, true);
-  float L = 0.f;
-  for (int s = tid; s < a.n_splits; s += 256) {
-    const int64_t pi = (base + s) * kDecMaxGroup + g;
-    const float m = a.ws_ml[pi * 2];
-    const float w = (M == NEG_INF) ? 0.f : fast_exp2((m - M) * a.scale_log2);  // m = -inf -> 0
-    wsh[s] = w;
-    L += w * a.ws_ml[pi * 2 + 1];
+#pragma unroll
+  for (int j = 0; j < kPerPart; ++j) {
+    const int sp = part + kParts * j;
+    ml[j][0] = NEG_INF;
+    ml[j][1] = 0.f;
+    if (gi < a.group && sp < a.n_splits) {
+      const int64_t pi = pbase + static_cast<int64_t>(sp) * kDecMaxGroup + gi;
+      ml[j][0] = a.ws_ml[pi * 2];
+      ml[j][1] = a.ws_ml[pi * 2 + 1];
+    }
+    M = fmaxf(M, ml[j][0]);
   }
-  L = block_reduce(L, red, false);  // also orders the wsh writes before the reads below
-  const int d = tid & (kD - 1);
-  const int part = tid >> 7;
-  float acc = 0.f;
-#pragma unroll 8
-  for (int s = part; s < a.n_splits; s += 2) acc += wsh[s] * a.ws_o[((base + s) * kDecMaxGroup + g) * kD + d];
-  if (part == 1) half_acc[d] = acc;
+  red[part * kDecMaxGroup + gi] = M;
   __syncthreads();
-  if (part == 0) {
-    acc += half_acc[d];
-    const float o = L > 0.f ? acc / L : 0.f;
-    a.out[static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(qh) * a.o_sh + d] = f32_to_bf16(o);
+  if (tid < kDecMaxGroup) {
+    float mm = NEG_INF;
+    for (int p2 = 0; p2 < kParts; ++p2) mm = fmaxf(mm, red[p2 * kDecMaxGroup + tid]);
+    sh_M[tid] = mm;
   }
+  __syncthreads();
+  float* wts = sh_o;  // [n_splits][16]
+  {
+    const float Mg = sh_M[gi];
+    float L = 0.f;
+#pragma unroll
+    for (int j = 0; j < kPerPart; ++j) {
+      const int sp = part + kParts * j;
+      const float wt = (Mg == NEG_INF) ? 0.f : fast_exp2((ml[j][0] - Mg) * c);  // m = -inf -> 0
+      if (sp < a.n_splits) wts[sp * kDecMaxGroup + gi] = wt;
+      L += wt * ml[j][1];
+    }
+    __syncthreads();  // every read of sh_M / red above is done
+    red[part * kDecMaxGroup + gi] = L;
+  }
+  __syncthreads();
+  if (tid < kDecMaxGroup) {
+    float ll = 0.f;
+    for (int p2 = 0; p2 < kParts; ++p2) ll += red[p2 * kDecMaxGroup + tid];
+    sh_L[tid] = ll;
+  }
+  __syncthreads();
+  if (owner) {
+    // out = sum_s w_s o_s / L, kBatch independent 16-byte loads in flight per thread
+    constexpr int kBatch = 32;
+    const float* po = a.ws_o + (pbase + gq) * kD + d4;
+    const int64_t sstride = static_cast<int64_t>(kDecMaxGroup) * kD;
+    f32x4 acc = f32x4{};
+    for (int s0 = 0; s0 < a.n_splits; s0 += kBatch) {
+      f32x4 buf[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j)
+        buf[j] = (s0 + j < a.n_splits) ? *reinterpret_cast<const f32x4*>(po + (s0 + j) * sstride) : f32x4{};
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j)
+        if (s0 + j < a.n_splits) acc += wts[(s0 + j) * kDecMaxGroup + gq] * buf[j];
+    }
+    const float Lg = sh_L[gq];
+    const float inv = Lg > 0.f ? 1.f / Lg : 0.f;
+    uint16_t* o = a.out + static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(h * a.group + gq) * a.o_sh + d4;
+    u32x2 pk;
+    pk[0] = pack_bf16x2(acc[0] * inv, acc[1] * inv);
+    pk[1] = pack_bf16x2(acc[2] * inv, acc[3] * inv);
+    *reinterpret_cast<u32x2*>(o) = pk;
+  }
+  if (tid == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Level count per page for one sequence of length N (decode rule, block_n = 16).
@@ -256,12 +332,9 @@ __global__ void decode_page_levels_kernel(int32_t* out, int n_pages, int N, Leve
   out[p] = levels_of(lt, max(0, (N - 1) - (p * kPage + kPage - 1)));
 }
 
-hipError_t launch_decode(const DecodeArgs& a, const MergeArgs& m, hipStream_t s) {
+hipError_t launch_decode(const DecodeArgs& a, hipStream_t s) {
   if (a.batch <= 0) return hipSuccess;
-  hipLaunchKernelGGL(decode_split_kernel, dim3(a.n_splits, a.hkv, a.batch), dim3(64), 0, s, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(decode_merge_kernel, dim3(m.hq, m.batch), dim3(256), 0, s, m);
+  hipLaunchKernelGGL(decode_kernel, dim3(a.n_splits, a.hkv, a.batch), dim3(kDecWaves * 64), 0, s, a);
   return hipGetLastError();
 }
 

@@ -19,8 +19,10 @@ constexpr int kPfLdsBytes = kPfStages * kPfStageBytes;
 
 // Decode geometry (block_n = one page).
 constexpr int kDecMaxGroup = 16;
-constexpr int kDecUnroll = 4;
-constexpr int kDecMaxSplits = 1024;
+constexpr int kDecUnroll = 4;      // pages in flight per wave
+constexpr int kDecWaves = 8;       // waves per workgroup (one split), 2 per SIMD
+constexpr int kDecMaxSplits = 256;
+constexpr int kDecCounterBytes = 256;  // counter region granularity in the workspace
 
 struct KvWriteArgs {
   uint16_t* k_cache;
@@ -61,6 +63,8 @@ struct PrefillArgs {
 struct DecodeArgs {
   const uint16_t* q;  // [B][Hq][128] (strided)
   int64_t q_sb, q_sh;
+  uint16_t* out;  // [B][Hq][128] (strided)
+  int64_t o_sb, o_sh;
   const uint16_t* k_cache;
   const uint16_t* v_cache;
   int num_pages;
@@ -74,24 +78,16 @@ struct DecodeArgs {
   const float* rope_cs;
   int layout;
   LevelTable lt;
-  float* ws_o;   // [B][Hkv][n_splits][16][128]
-  float* ws_ml;  // [B][Hkv][n_splits][16][2]
-};
-
-struct MergeArgs {
-  uint16_t* out;  // [B][Hq][128] (strided)
-  int64_t o_sb, o_sh;
-  const float* ws_o;
-  const float* ws_ml;
-  int batch, hq, hkv, group, n_splits;
-  float scale_log2;
+  uint32_t* counters;  // [B][Hkv], zero between calls
+  float* ws_ml;        // [B][Hkv][n_splits][16][2]
+  float* ws_o;         // [B][Hkv][n_splits][16][128]
 };
 
 hipError_t launch_kv_write(const KvWriteArgs& a, hipStream_t s);
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t s);
 hipError_t launch_prefill_tile_levels(int32_t* out, int n_row_tiles, int n_kblocks, int q_offset,
                                       const LevelTable& lt, hipStream_t s);
-hipError_t launch_decode(const DecodeArgs& a, const MergeArgs& m, hipStream_t s);
+hipError_t launch_decode(const DecodeArgs& a, hipStream_t s);
 hipError_t launch_decode_page_levels(int32_t* out, int n_pages, int seq_len, const LevelTable& lt,
                                      hipStream_t s);
 

@@ -81,8 +81,9 @@ int atf_kv_write_bf16(void* k_cache, void* v_cache, int num_pages, int num_kv_he
  * Windowed causal GQA prefill: out[b, i, h, :] = attention of query row i
  * (absolute position q_offset + i) over keys 0..q_offset+i of sequence b read
  * from the paged cache (nk keys present, q_offset + nq <= nk).  q/out are bf16
- * [batch][nq][num_q_heads][128] with element strides (last dim contiguous).
- * lse (nullable) receives fp32 [batch][num_q_heads][nq] natural-log
+ * [batch][nq][num_q_heads][128] with element strides (last dim contiguous;
+ * q 16-byte aligned with strides multiples of 8, out 8-byte aligned with
+ * strides multiples of 4).  lse (nullable) receives fp32 [batch][num_q_heads][nq] natural-log
  * log-sum-exp of the scaled scores.  Q is rotated with rope_cs at load.
  *
  * Replaces flash_attn.cute.interface._flash_attn_fwd(q, k, v, causal=True,
@@ -97,13 +98,21 @@ int atf_prefill_bf16(void* out, int64_t o_sb, int64_t o_st, int64_t o_sh, float*
                      const int32_t* zhi, float sm_scale, const float* rope_cs, int rope_max_pos,
                      int layout, void* stream);
 
-/* Bytes of fp32 workspace atf_decode_paged_bf16 needs for these sizes. */
+/*
+ * Bytes of device workspace atf_decode_paged_bf16 needs for these sizes: split
+ * partials plus one arrival counter per (sequence, kv head).  The workspace
+ * must be zero-filled once before its first use; every completed call leaves
+ * its counters at zero again, so the same buffer serves later calls of any
+ * size up to the one it was sized for.  Calls that share a workspace must be
+ * ordered on one stream (concurrent calls on one workspace race).
+ */
 size_t atf_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int max_seq_len);
 
 /*
  * Windowed split-KV decode: one query token per sequence at position
  * seq_lens[b] - 1 attending to keys 0..seq_lens[b]-1 of the paged cache.
- * q/out are bf16 [batch][num_q_heads][128] with element strides; seq_lens is a
+ * q/out are bf16 [batch][num_q_heads][128] with element strides (q: 16-byte
+ * aligned, strides multiples of 8; out: 8-byte aligned, strides multiples of 4); seq_lens is a
  * device int32 [batch] whose entries must not exceed max_seq_len.  The window
  * is quantized per page (block_n = 16): page p reads its first L(p) levels only.
  *

@@ -124,3 +124,31 @@ def test_hnd_layout_and_strided_q(dev):
     b = interface.single_decode_with_kv_cache(q.to(dev), k.transpose(0, 1).contiguous().to(dev),
                                               v.transpose(0, 1).contiguous().to(dev), kv_layout="HND")
     assert torch.equal(a.cpu(), b.cpu())
+
+
+def test_workspace_reuse_across_calls(dev):
+    """The cached workspace's arrival counters return to zero after each call:
+    a large call, a smaller one, then the large one again (bitwise equal)."""
+    from atflash import interface
+    g = torch.Generator().manual_seed(21)
+    big = [H.randn_bf16(s, g) for s in ((28, H.D), (6000, 4, H.D), (6000, 4, H.D))]
+    small = [H.randn_bf16(s, g) for s in ((28, H.D), (300, 4, H.D), (300, 4, H.D))]
+
+    def run(q, k, v):
+        return interface.single_decode_with_kv_cache(q.to(dev), k.to(dev), v.to(dev)).cpu()
+
+    a = run(*big)
+    s = run(*small)
+    b = run(*big)
+    assert torch.equal(a, b)
+    H.assert_close(s, H.decode_oracle(*small, 1e4, float("inf"), False), "small call between large ones")
+
+
+def test_split_count_cap_long_sequence(dev):
+    """One kv head and 70000 tokens: the split count hits its cap (256 splits)."""
+    g = torch.Generator().manual_seed(22)
+    q = H.randn_bf16((8, H.D), g)
+    k = H.randn_bf16((70000, 1, H.D), g)
+    v = H.randn_bf16((70000, 1, H.D), g)
+    out = _decode_single(q, k, v, 5e5, 2.0, True, dev)
+    H.assert_close(out, H.decode_oracle(q, k, v, 5e5, 2.0, True), "70000 tokens, 1 kv head")
