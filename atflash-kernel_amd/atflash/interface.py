@@ -61,7 +61,7 @@ def _flash_attn_fwd(q, k, v, causal=True, pack_gqa=None, atflash_window_zhi=None
                     rope=None, layout="half_split", q_offset=None):
     """Windowed causal GQA prefill.  Returns (out [B, Nq, Hq, 128] bf16,
     lse [B, Hq, Nq] fp32).  pack_gqa is accepted for interface compatibility;
-    the tile quantization does not depend on it (block_m = 64 positions)."""
+    the tile quantization does not depend on it ((block_m, block_n) = (32, 32))."""
     if not causal:
         raise ValueError("only causal attention is supported")
     B, Nq, Hq, D = q.shape

@@ -42,6 +42,17 @@ PEAK_BF16 = 2.5e15
 PEAK_HBM = 8.0e12
 
 
+def _traffic():
+    """HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE passes
+    (calibrated against a plain device copy), committed as profiles/traffic.json;
+    None if that file is absent."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
+
+
 def _events_time(fn, n):
     import torch
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
@@ -139,7 +150,7 @@ def slice_ratios(N):
     return out
 
 
-def cpu_baseline(N, samples=48):
+def cpu_baseline(N, samples=160):
     """The oracle on host cores for `samples` 32-row tiles spread over the 128K
     prefill (window k = 2), extrapolated to all N/32 tiles."""
     import torch
@@ -225,6 +236,18 @@ def main():
         t = res["decode"][name]["mean_ms"] * 1e-3
         dec[name] = {"bytes": nbytes, "GBps": nbytes / t / 1e9, "frac": nbytes / t / PEAK_HBM}
 
+    tr = _traffic()
+
+    def traffic_of(kernel, window):
+        try:
+            return tr["kernels"][kernel][window]["hbm_bytes"]
+        except (TypeError, KeyError):
+            return None
+    for name in roof:
+        roof[name]["traffic"] = traffic_of("prefill_kernel", name)
+    for name in dec:
+        dec[name]["traffic"] = traffic_of("decode_kernel", name)
+
     pre = res["prefill"]
     line = {
         "metric": "prefill ms + decode us/step @128K, Qwen2.5-7B shape, window ON vs OFF; %roofline",
@@ -244,11 +267,12 @@ def main():
                    "hq": HQ, "hkv": HKV, "head_dim": D, "rope_base": BASE, "seq_len": N,
                    "windows": ["off", "k=2", "k=64"]},
         "roofline": {"bound": "mfma", "achieved": roof["off"]["tflops"], "peak": PEAK_BF16 / 1e12,
-                     "unit": "TFLOP/s", "frac": roof["off"]["frac"], "traffic": None,
+                     "unit": "TFLOP/s", "frac": roof["off"]["frac"], "traffic": roof["off"]["traffic"],
                      "kernel": "atf::prefill_kernel, window OFF",
                      "per_window": roof},
         "roofline_decode": {"bound": "hbm", "achieved": dec["off"]["GBps"], "peak": PEAK_HBM / 1e9,
-                            "unit": "GB/s", "frac": dec["off"]["frac"], "per_window": dec},
+                            "unit": "GB/s", "frac": dec["off"]["frac"], "traffic": dec["off"]["traffic"],
+                            "kernel": "atf::decode_kernel, window OFF", "per_window": dec},
         "detail": {
             "prefill_ms": {n: pre[n]["median_ms"] for n in pre},
             "prefill_attn_kernel_ms": {n: attn[n]["median_ms"] for n in attn},

@@ -1,0 +1,186 @@
+"""Pin the fp32 oracle attention (oracle/attention.py) without trusting its code.
+
+Each check compares the oracle with something that shares no code with it: a
+textbook fp64 softmax attention, an fp64 cell-by-cell brute force of the window
+rule, an explicit K/V head repeat, complex-number RoPE, or the closed-form
+log-sum-exp merge.  Sizes are small so the whole file runs in seconds on CPU.
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import attention as OA
+from oracle import window_rule as WR
+
+D = 128
+
+
+def _rand(shape, seed):
+    return torch.randn(shape, generator=torch.Generator().manual_seed(seed), dtype=torch.float32)
+
+
+def _textbook_causal_fp64(q, k, v, q_offset=0):
+    """softmax(q k^T / sqrt(d) + causal mask) v in fp64, GQA by head index // group."""
+    b, hq, M, d = q.shape
+    hkv, N = k.shape[1], k.shape[2]
+    g = hq // hkv
+    out = torch.zeros((b, hq, M, d), dtype=torch.float64)
+    for bi in range(b):
+        for h in range(hq):
+            s = q[bi, h].double() @ k[bi, h // g].double().T / math.sqrt(d)
+            pos = torch.arange(q_offset, q_offset + M)[:, None]
+            s = s.masked_fill(torch.arange(N)[None, :] > pos, float("-inf"))
+            out[bi, h] = torch.softmax(s, dim=-1) @ v[bi, h // g].double()
+    return out
+
+
+INF_W = [float("inf")] * (D // 2)
+
+
+def test_window_off_equals_textbook_causal():
+    q, k, v = _rand((1, 4, 70, D), 1), _rand((1, 1, 70, D), 2), _rand((1, 1, 70, D), 3)
+    got = OA.ref_window_attn(q, k, v, INF_W, phase="prefill", block_m=16, block_n=8)
+    ref = _textbook_causal_fp64(q, k, v)
+    assert (got.double() - ref).abs().max().item() < 2e-6
+
+
+def test_window_off_bottom_right_causal_with_offset():
+    # 24 query rows at absolute positions 40..63 against 64 keys
+    q, k, v = _rand((1, 2, 24, D), 4), _rand((1, 2, 64, D), 5), _rand((1, 2, 64, D), 6)
+    got = OA.ref_window_attn(q, k, v, INF_W, phase="prefill", block_m=8, block_n=8, q_offset=40)
+    ref = _textbook_causal_fp64(q, k, v, q_offset=40)
+    assert (got.double() - ref).abs().max().item() < 2e-6
+
+
+@pytest.mark.parametrize("phase,M,bm,bn", [("prefill", 48, 16, 8), ("prefill", 37, 8, 16), ("decode", 1, 1, 16),
+                                           ("decode", 1, 1, 4)])
+def test_window_on_equals_cellwise_bruteforce(phase, M, bm, bn):
+    # base 1e4, k = 0.05: the widths span 0.6 .. 5000, so D_eff steps through
+    # every level within a few dozen keys
+    w = WR.wavelengths_sorted(D, 1e4, 0.05)
+    N = 48 if phase == "prefill" else 150
+    q, k, v = _rand((1, 4, M, D), 7), _rand((1, 2, N, D), 8), _rand((1, 2, N, D), 9)
+    if phase == "prefill":
+        q = q[:, :, :N]
+    got = OA.ref_window_attn(q, k, v, w, phase=phase, block_m=bm, block_n=bn)
+    ref = OA.naive_window_attn_fp64(q, k, v, w, phase=phase, block_m=bm, block_n=bn)
+    assert (got.double() - ref).abs().max().item() < 2e-6
+    # the case really exercises several prefix lengths
+    deffs = {WR.deff_of_zmin(z, w, D) for z in range(N)}
+    assert len(deffs) >= 5
+
+
+def test_window_changes_the_output():
+    """A planted mistake -- ignoring the window -- is visible at these sizes."""
+    w = WR.wavelengths_sorted(D, 1e4, 0.05)
+    q, k, v = _rand((1, 2, 48, D), 10), _rand((1, 1, 48, D), 11), _rand((1, 1, 48, D), 12)
+    on = OA.ref_window_attn(q, k, v, w, phase="prefill", block_m=16, block_n=8)
+    off = OA.ref_window_attn(q, k, v, INF_W, phase="prefill", block_m=16, block_n=8)
+    assert (on - off).abs().max().item() > 1e-2
+
+
+def test_query_chunks_equal_single_shot():
+    w = WR.wavelengths_sorted(D, 1e4, 0.05)
+    q, k, v = _rand((1, 2, 96, D), 13), _rand((1, 1, 96, D), 14), _rand((1, 1, 96, D), 15)
+    full = OA.ref_window_attn(q, k, v, w, phase="prefill", block_m=16, block_n=8)
+    for off in (0, 32, 64):
+        part = OA.ref_window_attn(q[:, :, off:off + 32], k, v, w, phase="prefill", block_m=16, block_n=8,
+                                  q_offset=off)
+        assert torch.equal(part, full[:, :, off:off + 32])
+
+
+def test_gqa_equals_explicit_repeat():
+    w = WR.wavelengths_sorted(D, 1e4, 0.05)
+    q, k, v = _rand((1, 6, 40, D), 16), _rand((1, 2, 40, D), 17), _rand((1, 2, 40, D), 18)
+    a = OA.ref_window_attn(q, k, v, w, phase="prefill", block_m=8, block_n=8)
+    kr, vr = k.repeat_interleave(3, dim=1), v.repeat_interleave(3, dim=1)
+    b = OA.ref_window_attn(q, kr, vr, w, phase="prefill", block_m=8, block_n=8)
+    assert (a - b).abs().max().item() < 1e-6
+
+
+def test_tile_rows_subset_matches_full():
+    w = WR.wavelengths_sorted(D, 1e4, 0.05)
+    q, k, v = _rand((1, 2, 64, D), 19), _rand((1, 1, 64, D), 20), _rand((1, 1, 64, D), 21)
+    full = OA.ref_window_attn(q, k, v, w, phase="prefill", block_m=16, block_n=8)
+    part = OA.ref_window_attn(q, k, v, w, phase="prefill", block_m=16, block_n=8, tile_rows=[16, 48])
+    for r in (16, 48):
+        assert torch.equal(part[:, :, r:r + 16], full[:, :, r:r + 16])
+    assert part[:, :, 0:16].abs().max().item() == 0.0
+
+
+def test_bf16_mode_is_an_anchor_near_fp32():
+    w = WR.wavelengths_sorted(D, 1e4, 2.0)
+    q, k, v = _rand((1, 4, 64, D), 22), _rand((1, 1, 64, D), 23), _rand((1, 1, 64, D), 24)
+    a = OA.ref_window_attn(q, k, v, w, phase="prefill", block_m=16, block_n=16)
+    b = OA.ref_window_attn(q, k, v, w, phase="prefill", block_m=16, block_n=16, mode="bf16")
+    assert b.dtype == torch.bfloat16
+    assert (a - b.float()).abs().max().item() < 2e-2
+
+
+def test_rope_hf_equals_complex_rotation():
+    x = _rand((3, 10, D), 25)
+    pos = torch.arange(100, 110)
+    inv = OA.inv_freq_closed_form(D, 1e4)
+    got = OA.rope_hf(x, pos, inv)
+    P = D // 2
+    z = torch.complex(x[..., :P].double(), x[..., P:].double())
+    ang = pos.double()[:, None] * inv.double()[None, :]
+    rz = z * torch.polar(torch.ones_like(ang), ang)
+    ref = torch.cat([rz.real, rz.imag], dim=-1)
+    assert (got.double() - ref).abs().max().item() < 1e-4
+    # the closed form of inv_freq: 1 / base^(2i/d)
+    assert inv[1].item() == pytest.approx(1e4 ** (-2 / D), rel=1e-6)
+
+
+def test_sorted_pair_layout_puts_long_wavelengths_first():
+    perm = OA.hf_to_sorted_pair_perm(D)
+    assert sorted(perm.tolist()) == list(range(D))
+    P = D // 2
+    for j in range(P):  # sorted pair j <- HF pair r = P-1-j
+        assert perm[2 * j].item() == P - 1 - j and perm[2 * j + 1].item() == 2 * P - 1 - j
+    # w'_j = k * 2 pi / inv_freq[P-1-j], descending
+    w = WR.wavelengths_sorted(D, 1e4, 2.0)
+    inv = OA.inv_freq_closed_form(D, 1e4).double()
+    for j in (0, 5, 40, P - 1):
+        assert w[j] == pytest.approx(2.0 * 2 * math.pi / inv[P - 1 - j].item(), rel=1e-6)
+    assert all(w[j] >= w[j + 1] for j in range(P - 1))
+    # a dot product restricted to the sorted prefix equals the sum over the
+    # corresponding HF pairs
+    a, b = _rand((D,), 26), _rand((D,), 27)
+    sa, sb = OA.to_sorted(a), OA.to_sorted(b)
+    for deff in (16, 48, 128):
+        pairs = [P - 1 - j for j in range(deff // 2)]
+        hf = sum(a[r] * b[r] + a[r + P] * b[r + P] for r in pairs)
+        assert (sa[:deff] @ sb[:deff]).item() == pytest.approx(hf.item(), rel=1e-5, abs=1e-5)
+
+
+def test_sliced_decode_equals_tile_rule_at_block_n_1():
+    """Slice tables of width 16 (one per level) reproduce phase="decode" with
+    block_n = 1, where each key's distance is its own age."""
+    w = WR.wavelengths_sorted(D, 1e4, 0.05)
+    N = 300
+    zhi = WR.zhi_table(w, D, N)
+    q, k, v = _rand((4, D), 28), _rand((N, 2, D), 29), _rand((N, 2, D), 30)
+    got, _ = OA.ref_decode_sliced(q, k, v, zhi, 16)
+    ref = OA.ref_window_attn(q[None, :, None, :], k.permute(1, 0, 2)[None], v.permute(1, 0, 2)[None], w,
+                             phase="decode", block_m=1, block_n=1)[0, :, 0]
+    assert (got - ref).abs().max().item() < 1e-5
+
+
+def test_lse_merge_equals_unsplit():
+    s = _rand((3, 200), 31) * 3
+    vv = _rand((200, D), 32)
+    full = torch.softmax(s.double(), dim=-1) @ vv.double()
+    bounds = [0, 17, 90, 200]
+    ms, ls, os_ = [], [], []
+    for a, b in zip(bounds[:-1], bounds[1:]):
+        sp = s[:, a:b].double()
+        m = sp.max(dim=-1).values
+        e = torch.exp(sp - m[:, None])
+        ms.append(m)
+        ls.append(e.sum(dim=-1))
+        os_.append((e @ vv[a:b].double()) / e.sum(dim=-1, keepdim=True))
+    m, l_tot, o = OA.lse_merge(torch.stack(ms), torch.stack(ls), torch.stack(os_))
+    assert (o - full).abs().max().item() < 1e-12
+    assert torch.allclose(m + torch.log(l_tot), torch.logsumexp(s.double(), dim=-1))
