@@ -121,13 +121,14 @@ def test_tile_levels_match_oracle_segments(dev):
     """Per-(32-row, 32-key) tile level counts computed on the GPU equal
     D_eff/16 from the oracle's deff_segments."""
     from atflash import atflash_window as AW, ops
-    for base, k_ret, N, q_off in [(1e7, 2.0, 8192, 0), (5e5, 2.0, 4096, 1024), (1e4, 0.5, 2048, 64)]:
+    for base, k_ret, N, q_off in [(1e7, 2.0, 8192, 0), (5e5, 2.0, 4096, 1024), (1e4, 0.5, 2048, 64),
+                                  (1e7, 2.0, 131072, 0), (1e7, 64.0, 131072, 8192)]:
         zhi = AW.window_zhi_from_kret(H.D, base, k_ret, 1 << 20)
         w = WR.wavelengths_sorted(H.D, base, k_ret)
         nrt = (N - q_off) // 32
         nkb = N // 32
         got = ops.prefill_tile_levels(nrt, nkb, q_off, zhi, dev).cpu()
-        for rt in range(0, nrt, 7):
+        for rt in list(range(0, nrt, max(7, nrt // 24))) + [nrt - 1]:
             q0 = q_off + 32 * rt
             segs = WR.deff_segments("prefill", q0, min(q0 + 32, N), 32, 32, N, w, H.D)
             for n0, n1, deff in segs:
