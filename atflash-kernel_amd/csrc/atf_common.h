@@ -42,6 +42,8 @@ typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
 typedef __attribute__((ext_vector_type(4))) short s16x4;
 typedef __attribute__((ext_vector_type(16))) float f32x16;
 typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
 typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
 
@@ -83,8 +85,12 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
+// Two floats -> packed bf16 pair (lo in bits 0-15), round to nearest even.  The
+// two-element vector conversion selects one v_cvt_pk_bf16_f32; converting the
+// halves separately and or-ing them costs four instructions.
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+  const f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
 // Unpack 8 bf16 (16 B) into floats.
@@ -104,18 +110,28 @@ __device__ __forceinline__ u32x4 pack8(const float* f) {
 }
 
 // Rotate-half RoPE on one 8-pair chunk: lane keeps the first half
-// (x1 c - x2 s) or the second half (x2 c + x1 s).  cs holds (cos, sin) per pair.
-__device__ __forceinline__ u32x4 rope_half(const u32x4& x1v, const u32x4& x2v, const float* cs,
-                                          bool second) {
+// (x1 c - x2 s) or the second half (x2 c + x1 s), times `scale`.  cs holds
+// (cos, sin) per pair.
+__device__ __forceinline__ u32x4 rope_half(const u32x4& x1v, const u32x4& x2v, const float* cs, bool second,
+                                          float scale = 1.f) {
   float x1[8], x2[8], y[8];
   unpack8(x1v, x1);
   unpack8(x2v, x2);
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const float c = cs[2 * i], s = cs[2 * i + 1];
-    y[i] = second ? (x2[i] * c + x1[i] * s) : (x1[i] * c - x2[i] * s);
+    y[i] = scale * (second ? (x2[i] * c + x1[i] * s) : (x1[i] * c - x2[i] * s));
   }
   return pack8(y);
+}
+
+// 8 bf16 times `scale`, rounded back to bf16.
+__device__ __forceinline__ u32x4 scale8(const u32x4& xv, float scale) {
+  float x[8];
+  unpack8(xv, x);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] *= scale;
+  return pack8(x);
 }
 
 __device__ __forceinline__ u32x4 ldg16(const void* p) {

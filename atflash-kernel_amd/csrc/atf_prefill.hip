@@ -20,8 +20,12 @@
 //   Per (wave, kb) the QK contraction runs over the first L = D_eff/16 levels
 //   only, and the workgroup copies only the levels its first wave needs, so the
 //   out-of-window K levels never enter LDS.  Q is rotated (RoPE) at load.
-//   Online softmax with a lazily updated reference max: O and l are rescaled only
-//   when a row's max grows by more than 2^8 in exp2 units, so P <= 256.
+//   Online softmax in log2 units with a lazily updated reference max m_ref: Q is
+//   scaled by sm_scale*log2(e) when it is loaded (rounded to bf16 once, as it is
+//   anyway after RoPE), and every QK chain starts from -m_ref (a register tuple
+//   used as the C operand of its first MFMA), so the MFMAs return S - m_ref and
+//   P = exp2 of the accumulator directly.  O and l are rescaled only when a
+//   row's max grows past m_ref by more than 8, so P <= 256.
 #include "atf_launch.h"
 
 namespace atf {
@@ -29,6 +33,7 @@ namespace atf {
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
 constexpr float kLazyRescaleLog2 = 8.0f;
+constexpr float kLn2 = 0.6931471805599453f;
 
 __device__ __forceinline__ float pair_max(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -43,8 +48,18 @@ __device__ __forceinline__ float pair_sum(float x) {
 // Written as the VOP3P instruction: the clang builtin for the bf16 dot2 lowers
 // to the VOP2 form with the same source register for every element of a
 // vector (ROCm 7.2), which sums the wrong values.
+//
+// The dot instruction writes its result through the dot pipeline: a following
+// dot of the same opcode may take it as its accumulator at once, but any other
+// VALU read needs 3 wait states, which the compiler cannot insert for inline
+// asm.  The last link of each tile's chain therefore carries its own wait
+// states inside the same statement (nothing can be scheduled in between).
 __device__ __forceinline__ float dot2_ones(uint32_t x, float acc) {
   asm("v_dot2_f32_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(x), "v"(0x3f803f80u));
+  return acc;
+}
+__device__ __forceinline__ float dot2_ones_last(uint32_t x, float acc) {
+  asm("v_dot2_f32_bf16 %0, %1, %2, %0\n\ts_nop 4" : "+v"(acc) : "v"(x), "v"(0x3f803f80u));
   return acc;
 }
 
@@ -118,8 +133,9 @@ __device__ __forceinline__ void pf_load_tile(const PrefillArgs& a, int b, int kv
 // chain, the operand of level l+1 read from LDS while level l's MFMA runs.  `a`
 // holds the level-0 operand on entry.
 template <int L>
-__device__ __forceinline__ f32x16 qk_chain(const lds_u8* kbase, const u32x4 (&Qf)[kLevels], bf16x8 a) {
-  f32x16 S = f32x16{};
+__device__ __forceinline__ f32x16 qk_chain(const lds_u8* kbase, const u32x4 (&Qf)[kLevels], bf16x8 a,
+                                          const f32x16& C) {
+  f32x16 S = C;
 #pragma unroll
   for (int l = 0; l < L; ++l) {
     bf16x8 an = a;
@@ -135,9 +151,9 @@ __device__ __forceinline__ f32x16 qk_chain(const lds_u8* kbase, const u32x4 (&Qf
 // operands one level ahead.
 template <int L>
 __device__ __forceinline__ void qk_pair(const lds_u8* k0, const lds_u8* k1, const u32x4 (&Qf)[kLevels], bf16x8 a,
-                                        bf16x8 b, f32x16& S0, f32x16& S1) {
-  S0 = f32x16{};
-  S1 = f32x16{};
+                                        bf16x8 b, const f32x16& C, f32x16& S0, f32x16& S1) {
+  S0 = C;
+  S1 = C;
 #pragma unroll
   for (int l = 0; l < L; ++l) {
     bf16x8 an = a, bn = b;
@@ -153,37 +169,39 @@ __device__ __forceinline__ void qk_pair(const lds_u8* k0, const lds_u8* k1, cons
   }
 }
 
-__device__ __forceinline__ f32x16 qk_one(int L, const lds_u8* kbase, const u32x4 (&Qf)[kLevels], bf16x8 a) {
+__device__ __forceinline__ f32x16 qk_one(int L, const lds_u8* kbase, const u32x4 (&Qf)[kLevels], bf16x8 a,
+                                        const f32x16& C) {
   switch (L) {
-    case 8: return qk_chain<8>(kbase, Qf, a);
-    case 7: return qk_chain<7>(kbase, Qf, a);
-    case 6: return qk_chain<6>(kbase, Qf, a);
-    case 5: return qk_chain<5>(kbase, Qf, a);
-    case 4: return qk_chain<4>(kbase, Qf, a);
-    case 3: return qk_chain<3>(kbase, Qf, a);
-    case 2: return qk_chain<2>(kbase, Qf, a);
-    default: return qk_chain<1>(kbase, Qf, a);
+    case 8: return qk_chain<8>(kbase, Qf, a, C);
+    case 7: return qk_chain<7>(kbase, Qf, a, C);
+    case 6: return qk_chain<6>(kbase, Qf, a, C);
+    case 5: return qk_chain<5>(kbase, Qf, a, C);
+    case 4: return qk_chain<4>(kbase, Qf, a, C);
+    case 3: return qk_chain<3>(kbase, Qf, a, C);
+    case 2: return qk_chain<2>(kbase, Qf, a, C);
+    default: return qk_chain<1>(kbase, Qf, a, C);
   }
 }
 
-// S^T for the two 32-key blocks of a tile with level counts L0 (far) and L1
-// (near); a0/a1 hold their level-0 operands.
+// S^T + C for the two 32-key blocks of a tile with level counts L0 (far) and
+// L1 (near); a0/a1 hold their level-0 operands.
 __device__ __forceinline__ void qk_tile(int L0, int L1, const lds_u8* k0, const lds_u8* k1,
-                                        const u32x4 (&Qf)[kLevels], bf16x8 a0, bf16x8 a1, f32x16& S0, f32x16& S1) {
+                                        const u32x4 (&Qf)[kLevels], bf16x8 a0, bf16x8 a1, const f32x16& C,
+                                        f32x16& S0, f32x16& S1) {
   if (L0 == L1) {
     switch (L0) {
-      case 8: qk_pair<8>(k0, k1, Qf, a0, a1, S0, S1); break;
-      case 7: qk_pair<7>(k0, k1, Qf, a0, a1, S0, S1); break;
-      case 6: qk_pair<6>(k0, k1, Qf, a0, a1, S0, S1); break;
-      case 5: qk_pair<5>(k0, k1, Qf, a0, a1, S0, S1); break;
-      case 4: qk_pair<4>(k0, k1, Qf, a0, a1, S0, S1); break;
-      case 3: qk_pair<3>(k0, k1, Qf, a0, a1, S0, S1); break;
-      case 2: qk_pair<2>(k0, k1, Qf, a0, a1, S0, S1); break;
-      default: qk_pair<1>(k0, k1, Qf, a0, a1, S0, S1); break;
+      case 8: qk_pair<8>(k0, k1, Qf, a0, a1, C, S0, S1); break;
+      case 7: qk_pair<7>(k0, k1, Qf, a0, a1, C, S0, S1); break;
+      case 6: qk_pair<6>(k0, k1, Qf, a0, a1, C, S0, S1); break;
+      case 5: qk_pair<5>(k0, k1, Qf, a0, a1, C, S0, S1); break;
+      case 4: qk_pair<4>(k0, k1, Qf, a0, a1, C, S0, S1); break;
+      case 3: qk_pair<3>(k0, k1, Qf, a0, a1, C, S0, S1); break;
+      case 2: qk_pair<2>(k0, k1, Qf, a0, a1, C, S0, S1); break;
+      default: qk_pair<1>(k0, k1, Qf, a0, a1, C, S0, S1); break;
     }
   } else {
-    S0 = qk_one(L0, k0, Qf, a0);
-    S1 = qk_one(L1, k1, Qf, a1);
+    S0 = qk_one(L0, k0, Qf, a0, C);
+    S1 = qk_one(L1, k1, Qf, a1, C);
   }
 }
 
@@ -220,7 +238,8 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
   const int t_end =
       (lr0 < a.nq) ? min(n_ktiles, (a.q_offset + min(a.nq, lr0 + kPfRowsWave) - 1) / kPfTileN + 1) : 0;
 
-  // ---- Q fragments (B operand of S^T = K Q^T), RoPE applied at load ----
+  // ---- Q fragments (B operand of S^T = K Q^T), with RoPE and the log2-unit
+  // softmax scale applied at load ----
   u32x4 Qf[kLevels];
   const bool second = lane >= 32;
   const int row = lr0 + (lane & 31);
@@ -236,9 +255,9 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
         if (a.rope_cs != nullptr) {
           float cs[16];
           load_cs8(a.rope_cs, a.q_offset + row, c0, cs);
-          v = rope_half(ldg16(qrow + c0), ldg16(qrow + c1), cs, second);
+          v = rope_half(ldg16(qrow + c0), ldg16(qrow + c1), cs, second, a.scale_log2);
         } else {
-          v = ldg16(qrow + (second ? c1 : c0));
+          v = scale8(ldg16(qrow + (second ? c1 : c0)), a.scale_log2);
         }
       }
       Qf[l] = v;
@@ -249,9 +268,9 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
 #pragma unroll
   for (int db = 0; db < 4; ++db) O[db] = f32x16{};
   const float NEG_INF = -__builtin_huge_valf();
-  float m_ref = NEG_INF;  // reference max of the exponentials (raw score units)
+  float m_ref = 0.f;      // reference max (log2 units), set by the first tile
   float l_run = 0.f;      // this lane's partial row sum relative to m_ref
-  const float c = a.scale_log2;
+  f32x16 Cm = f32x16{};   // -m_ref in every element
   const int T = t_end_wg;
 #ifndef ATF_PF_GROUP
 #define ATF_PF_GROUP(w) ((w) >> 2)
@@ -331,7 +350,7 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
       // (unused when the wave has no tile t).
       const int L0 = w_far.advance(a.lt, t);
       const int L1 = w_near.advance(a.lt, t);
-      qk_tile(L0, L1, kbase, kbase + 2 * 4096, Qf, a0, a1, S[0], S[1]);
+      qk_tile(L0, L1, kbase, kbase + 2 * 4096, Qf, a0, a1, Cm, S[0], S[1]);
     }
 #ifndef ATF_PF_NO_PRIO
     __builtin_amdgcn_s_setprio(0);
@@ -357,15 +376,27 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
         }
       }
       mx = pair_max(mx);
-      const bool grow = mx * c > m_ref * c + kLazyRescaleLog2;
+      // S already holds score - m_ref.  On the first tile (key 0 is visible to
+      // every row, so mx is finite) and wherever the max grew past m_ref by more
+      // than 8, m_ref moves up to the max: O and l are rescaled and this tile's
+      // scores shifted by the same delta (0 for the other lanes of the wave).
+      const bool grow = (t == 0) || mx > kLazyRescaleLog2;
       if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-        const float alpha = grow ? fast_exp2((m_ref - mx) * c) : 1.f;  // m_ref = -inf -> 0
-        if (grow) m_ref = mx;
-        l_run *= alpha;
+        const float delta = grow ? mx : 0.f;
+        if (t > 0) {
+          const float alpha = fast_exp2(-delta);
+          l_run *= alpha;
 #pragma unroll
-        for (int db = 0; db < 4; ++db) O[db] *= alpha;
+          for (int db = 0; db < 4; ++db) O[db] *= alpha;
+        }
+        m_ref += delta;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) Cm[i] = -m_ref;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) S[kb][r] -= delta;
       }
-      const float msc = (m_ref == NEG_INF) ? 0.f : m_ref * c;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
@@ -373,10 +404,10 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
           u32x4 pk;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float p0 = fast_exp2(__builtin_fmaf(S[kb][8 * hs + 2 * i], c, -msc));
-            const float p1 = fast_exp2(__builtin_fmaf(S[kb][8 * hs + 2 * i + 1], c, -msc));
+            const float p0 = fast_exp2(S[kb][8 * hs + 2 * i]);
+            const float p1 = fast_exp2(S[kb][8 * hs + 2 * i + 1]);
             pk[i] = pack_bf16x2(p0, p1);
-            l_run = dot2_ones(pk[i], l_run);
+            l_run = (kb == 1 && hs == 1 && i == 3) ? dot2_ones_last(pk[i], l_run) : dot2_ones(pk[i], l_run);
           }
           Pf[2 * kb + hs] = __builtin_bit_cast(bf16x8, pk);
         }
@@ -427,7 +458,7 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
     }
     if (a.lse != nullptr && lane < 32) {
       a.lse[(static_cast<int64_t>(b) * a.hq + h) * a.nq + row] =
-          (l > 0.f) ? m_ref * a.sm_scale + __logf(l) : NEG_INF;
+          (l > 0.f) ? m_ref * kLn2 + __logf(l) : NEG_INF;
     }
   }
 }

@@ -1,0 +1,199 @@
+"""CPU checks on the gfx950 assembly of the HIP kernels.
+
+The prefill kernel issues some instructions through inline asm (LDS operand
+reads with explicit waits, the bf16 dot2 row sums).  The compiler schedules
+around inline asm without knowing its latencies, so two mistakes compile
+silently and only show up as wrong numbers on the GPU:
+
+* a register written by an inline ``ds_read`` is read, copied or overwritten
+  before the ``s_waitcnt lgkmcnt`` that covers the read (the copy sees stale
+  data);
+* the result of ``v_dot2_f32_bf16`` (written through the dot pipeline) is read
+  by a different VALU instruction fewer than 3 wait states later.
+
+These tests compile each kernel source to device assembly with the library's own
+flags and scan it for both.  The scanners are first run on small snippets in
+which the mistake is planted, so a scanner that finds nothing is known to be
+able to find something.
+"""
+import os
+import re
+import shutil
+import subprocess
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(ROOT, "atflash-kernel_amd")
+
+_REG = re.compile(r"\b([va])(\d+)\b|\b([va])\[(\d+):(\d+)\]")
+
+
+def _regs(text):
+    out = set()
+    for m in _REG.finditer(text):
+        if m.group(1):
+            out.add((m.group(1), int(m.group(2))))
+        else:
+            out.update((m.group(3), r) for r in range(int(m.group(4)), int(m.group(5)) + 1))
+    return out
+
+
+def _instructions(asm):
+    """(line number, instruction text) for every instruction, comments dropped."""
+    out = []
+    for i, raw in enumerate(asm.split("\n"), 1):
+        s = raw.split(";")[0].strip()
+        if s and not s.startswith(".") and not s.endswith(":"):
+            out.append((i, s))
+    return out
+
+
+def lds_read_hazards(asm):
+    """Instructions touching the destination of an LDS read that no
+    s_waitcnt lgkmcnt has retired yet (linear scan; LDS and scalar-memory
+    operations retire in issue order for this purpose)."""
+    pending, found = [], []
+    for i, s in _instructions(asm):
+        op = s.split()[0]
+        args = s[len(op):]
+        if op == "s_waitcnt":
+            m = re.search(r"lgkmcnt\((\d+)\)", args)
+            if m:
+                n = int(m.group(1))
+                pending = pending[len(pending) - n:] if 0 < n < len(pending) else ([] if n == 0 else pending)
+            continue
+        touched = _regs(args)
+        for ln, dst in pending:
+            if dst and touched & dst:
+                found.append((i, s, ln))
+        if op.startswith(("ds_read", "ds_load")):
+            pending.append((i, _regs(args.split(",")[0])))
+        elif op.startswith(("ds_", "s_load", "s_buffer_load")):
+            pending.append((i, None))
+    return found
+
+
+def dot_hazards(asm, need=3):
+    """Reads of a v_dot2 result, other than as the accumulator of the next dot
+    of the same opcode, within `need` wait states of the write."""
+    ins = _instructions(asm)
+    found = []
+    for j, (i, s) in enumerate(ins):
+        if not s.startswith("v_dot2"):
+            continue
+        dst = s.split()[1].rstrip(",")
+        ws = 0
+        for i2, s2 in ins[j + 1:]:
+            op2 = s2.split()[0]
+            if op2 == "s_nop":
+                ws += int(s2.split()[1], 0) + 1
+            else:
+                ops = [o.strip() for o in s2[len(op2):].split(",")]
+                srcs = ops[1:] if op2.startswith("v_") else ops
+                if dst in srcs:
+                    if not (op2 == s.split()[0] and srcs.index(dst) == len(srcs) - 1):
+                        found.append((i2, s2, i))
+                    break
+                if ops and ops[0] == dst:
+                    break
+                ws += 1
+            if ws >= need:
+                break
+    return found
+
+
+# ------------------------------------------------------------ scanner self-tests
+
+def test_lds_scanner_finds_a_copy_before_the_wait():
+    bad = """
+        ds_read_b128 v[4:7], v1 offset:0
+        v_mov_b64_e32 v[20:21], v[4:5]
+        s_waitcnt lgkmcnt(0)
+    """
+    good = """
+        ds_read_b128 v[4:7], v1 offset:0
+        ds_read_b128 v[8:11], v1 offset:512
+        s_waitcnt lgkmcnt(1)
+        v_mov_b64_e32 v[20:21], v[4:5]
+        s_waitcnt lgkmcnt(0)
+        v_mov_b64_e32 v[22:23], v[8:9]
+    """
+    early = """
+        ds_read_b128 v[4:7], v1 offset:0
+        ds_read_b128 v[8:11], v1 offset:512
+        s_waitcnt lgkmcnt(1)
+        v_mov_b64_e32 v[22:23], v[8:9]
+    """
+    assert len(lds_read_hazards(bad)) == 1
+    assert lds_read_hazards(good) == []
+    assert len(lds_read_hazards(early)) == 1
+
+
+def test_dot_scanner_finds_an_early_read():
+    bad = """
+        v_dot2_f32_bf16 v10, v2, v3, v10
+        v_add_f32_e32 v11, v10, v11
+    """
+    chained = """
+        v_dot2_f32_bf16 v10, v2, v3, v10
+        v_dot2_f32_bf16 v10, v4, v3, v10
+        s_nop 4
+        v_add_f32_e32 v11, v10, v11
+    """
+    as_source_ab = """
+        v_dot2_f32_bf16 v10, v2, v3, v10
+        v_dot2_f32_bf16 v12, v10, v3, v12
+    """
+    assert len(dot_hazards(bad)) == 1
+    assert dot_hazards(chained) == []
+    assert len(dot_hazards(as_source_ab)) == 1
+
+
+# ------------------------------------------------------------ the kernels
+
+def _hipcc_or_skip():
+    sys.path.insert(0, PKG)
+    import build as B  # atflash-kernel_amd/build.py
+    if not os.path.exists(B.HIPCC) and shutil.which(B.HIPCC) is None:
+        pytest.skip("hipcc not available")
+    return B
+
+
+@pytest.fixture(scope="module")
+def kernel_asm(tmp_path_factory):
+    B = _hipcc_or_skip()
+    out = {}
+    tmp = tmp_path_factory.mktemp("asm")
+    for src in B.sources():
+        if not src.endswith(".hip"):
+            continue
+        dst = os.path.join(tmp, os.path.basename(src) + ".s")
+        flags = [f for f in B.COMMON if not f.startswith("-Rpass")]
+        cmd = [B.HIPCC, *flags, "-I", B.CSRC, "--cuda-device-only", "-S", src, "-o", dst]
+        p = subprocess.run(cmd, capture_output=True, text=True)
+        assert p.returncode == 0, p.stderr
+        with open(dst) as f:
+            out[os.path.basename(src)] = f.read()
+    assert "atf_prefill.hip" in out and "atf_decode.hip" in out
+    return out
+
+
+def test_no_lds_read_hazards(kernel_asm):
+    for name, asm in kernel_asm.items():
+        assert lds_read_hazards(asm) == [], name
+
+
+def test_no_dot_result_hazards(kernel_asm):
+    for name, asm in kernel_asm.items():
+        assert dot_hazards(asm) == [], name
+
+
+def test_prefill_kernel_does_not_spill(kernel_asm):
+    asm = kernel_asm["atf_prefill.hip"]
+    # kernel metadata: one "- .agpr_count" block per kernel, holding .name and .vgpr_spill_count
+    blocks = [b for b in asm.split("  - .agpr_count:") if re.search(r"\.name:\s+_ZN3atf14prefill_kernel", b)]
+    assert len(blocks) == 1, "prefill_kernel metadata not found"
+    spill = re.search(r"\.vgpr_spill_count:\s+(\d+)", blocks[0])
+    assert spill and int(spill.group(1)) == 0
