@@ -24,6 +24,11 @@
 
 namespace atf {
 
+// s_waitcnt immediate for vmcnt(0) alone (gfx9 encoding: vmcnt bits 3:0 and
+// 15:14, expcnt 6:4, lgkmcnt 11:8), issued through the builtin so the
+// compiler's own wait insertion accounts for it.
+constexpr int kWaitVm = 0x0F70;
+
 // max / sum over the 4 lanes {l, l^16, l^32, l^48} that hold one query head.
 __device__ __forceinline__ float quad_max(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -78,13 +83,13 @@ __device__ __forceinline__ void dec_load_page(const DecodeArgs& a, int b, int h,
 // two waves per SIMD: at most 256 registers per wave
 __global__ __launch_bounds__(kDecWaves * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void decode_kernel(DecodeArgs a) {
-  // wave partials; in the merging workgroup, afterwards, the split weights
+  // wave partials; in the merging workgroup, afterwards, the partial merges of
+  // up to 8 threads per (query head, dims) (o in sh_o, m and l in red)
   __shared__ __attribute__((aligned(16))) float sh_o[kDecWaves * kDecMaxGroup * kD];
   __shared__ float sh_m[kDecWaves * kDecMaxGroup], sh_l[kDecWaves * kDecMaxGroup];
   __shared__ float red[kDecWaves * 64];
-  __shared__ float sh_M[kDecMaxGroup], sh_L[kDecMaxGroup];
   __shared__ int sh_last;
-  static_assert(kDecMaxSplits * kDecMaxGroup <= kDecWaves * kDecMaxGroup * kD, "split weights must fit sh_o");
+  static_assert(kDecWaves >= 8 && kDecWaves * 64 >= 2 * 8 * kDecMaxGroup, "merge staging must fit sh_o and red");
 
   const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x;
@@ -228,22 +233,29 @@ void decode_kernel(DecodeArgs a) {
         acc += wt * *reinterpret_cast<const f32x4*>(&sh_o[(w * kDecMaxGroup + gq) * kD + d4]);
       }
     }
+    // Agent-scope stores: written through to the device coherence point, so no
+    // L2 write-back is needed before the arrival count below.
     const int64_t pi = pbase + static_cast<int64_t>(s) * kDecMaxGroup + gq;
-    *reinterpret_cast<f32x4*>(a.ws_o + pi * kD + d4) = acc;
+    float* po = a.ws_o + pi * kD + d4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) __hip_atomic_store(po + i, acc[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (d4 == 0) {
-      a.ws_ml[pi * 2 + 0] = M;
-      a.ws_ml[pi * 2 + 1] = L;
+      __hip_atomic_store(a.ws_ml + pi * 2 + 0, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.ws_ml + pi * 2 + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 
   // ---- arrival: the last split of (b, h) to finish merges all splits ----
-  // One release per workgroup: the barrier orders every wave's partial stores
-  // before thread 0's agent-scope release increment (each device-scope fence
-  // writes back the XCD's L2, so it is issued once, not per wave).
+  // The partials were stored at agent scope, and the barrier waits until every
+  // wave's stores have completed there, so thread 0's increment needs no
+  // release fence: a device-scope release writes back the whole XCD L2, and
+  // with 32 workgroups per XCD finishing together those write-backs serialize.
+  // (The workgroup barrier alone does not wait for stores: vmcnt(0) is explicit.)
+  __builtin_amdgcn_s_waitcnt(kWaitVm);
   __syncthreads();
   uint32_t* cnt = a.counters + (static_cast<int64_t>(b) * a.hkv + h);
   if (tid == 0) {
-    const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int last = (old == static_cast<uint32_t>(a.n_splits - 1)) ? 1 : 0;
     if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // the other splits' partials are visible
     sh_last = last;
@@ -251,76 +263,77 @@ void decode_kernel(DecodeArgs a) {
   __syncthreads();
   if (!sh_last) return;
 
-  // split weights w_s = exp2((m_s - M) c) and L = sum_s w_s l_s per query head;
-  // thread (gi, part) holds the (m, l) of splits part, part + 32, ... in registers
-  constexpr int kParts = kDecWaves * 64 / kDecMaxGroup;
-  constexpr int kPerPart = (kDecMaxSplits + kParts - 1) / kParts;
-  const int gi = tid & (kDecMaxGroup - 1), part = tid >> 4;
-  float ml[kPerPart][2];
-  float M = NEG_INF;
+  // ---- merge of the split partials (the last workgroup of (b, h) only) ----
+  // Thread t takes query head gq, dims d4..d4+3 and every H-th split starting at
+  // hh, with H threads per (head, dims) so that all 512 threads load.  It loads
+  // the (m, l) and o of up to kBatch splits before using any of them, so with up
+  // to 32 splits per thread the merge costs one memory round trip; more splits
+  // are folded in batch by batch with a running max.  The H partial merges of a
+  // (head, dims) are then combined through LDS.
+  constexpr int kBatch = 32;
+  const int H = (a.group <= 2) ? 8 : (a.group <= 4) ? 4 : (a.group <= 8) ? 2 : 1;
+  const int mr = tid >> 5;  // 0..15
+  const int mg = mr / H, hh = mr - (mr / H) * H;
+  const int md4 = 4 * (tid & 31);
+  const bool mact = mg < a.group;
+  float m_t = NEG_INF, L_t = 0.f;
+  f32x4 acc_t = f32x4{};
+  if (mact) {
+    for (int j0 = hh; j0 < a.n_splits; j0 += kBatch * H) {
+      f32x2 mlv[kBatch];
+      f32x4 ov[kBatch];
 #pragma unroll
-  for (int j = 0; j < kPerPart; ++j) {
-    const int sp = part + kParts * j;
-    ml[j][0] = NEG_INF;
-    ml[j][1] = 0.f;
-    if (gi < a.group && sp < a.n_splits) {
-      const int64_t pi = pbase + static_cast<int64_t>(sp) * kDecMaxGroup + gi;
-      ml[j][0] = a.ws_ml[pi * 2];
-      ml[j][1] = a.ws_ml[pi * 2 + 1];
+      for (int j = 0; j < kBatch; ++j) {
+        const int sp = j0 + j * H;
+        mlv[j] = f32x2{NEG_INF, 0.f};
+        ov[j] = f32x4{};
+        if (sp < a.n_splits) {
+          const int64_t pi = pbase + static_cast<int64_t>(sp) * kDecMaxGroup + mg;
+          mlv[j] = *reinterpret_cast<const f32x2*>(a.ws_ml + pi * 2);
+          ov[j] = *reinterpret_cast<const f32x4*>(a.ws_o + pi * kD + md4);
+        }
+      }
+      float mb = m_t;
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) mb = fmaxf(mb, mlv[j][0]);
+      if (mb != NEG_INF) {
+        const float r = fast_exp2((m_t - mb) * c);  // m_t = -inf -> 0
+        L_t *= r;
+        acc_t *= r;
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+          const float wt = fast_exp2((mlv[j][0] - mb) * c);  // empty split: m = -inf -> 0
+          L_t += wt * mlv[j][1];
+          acc_t += wt * ov[j];
+        }
+        m_t = mb;
+      }
     }
-    M = fmaxf(M, ml[j][0]);
-  }
-  red[part * kDecMaxGroup + gi] = M;
-  __syncthreads();
-  if (tid < kDecMaxGroup) {
-    float mm = NEG_INF;
-    for (int p2 = 0; p2 < kParts; ++p2) mm = fmaxf(mm, red[p2 * kDecMaxGroup + tid]);
-    sh_M[tid] = mm;
+    *reinterpret_cast<f32x4*>(&sh_o[(hh * kDecMaxGroup + mg) * kD + md4]) = acc_t;
+    if (md4 == 0) {
+      red[hh * kDecMaxGroup + mg] = m_t;
+      red[8 * kDecMaxGroup + hh * kDecMaxGroup + mg] = L_t;
+    }
   }
   __syncthreads();
-  float* wts = sh_o;  // [n_splits][16]
-  {
-    const float Mg = sh_M[gi];
+  if (mact && hh == 0) {
+    float M = NEG_INF;
+    for (int h2 = 0; h2 < H; ++h2) M = fmaxf(M, red[h2 * kDecMaxGroup + mg]);
     float L = 0.f;
-#pragma unroll
-    for (int j = 0; j < kPerPart; ++j) {
-      const int sp = part + kParts * j;
-      const float wt = (Mg == NEG_INF) ? 0.f : fast_exp2((ml[j][0] - Mg) * c);  // m = -inf -> 0
-      if (sp < a.n_splits) wts[sp * kDecMaxGroup + gi] = wt;
-      L += wt * ml[j][1];
+    f32x4 o = f32x4{};
+    if (M != NEG_INF) {
+      for (int h2 = 0; h2 < H; ++h2) {
+        const float wt = fast_exp2((red[h2 * kDecMaxGroup + mg] - M) * c);
+        L += wt * red[8 * kDecMaxGroup + h2 * kDecMaxGroup + mg];
+        o += wt * *reinterpret_cast<const f32x4*>(&sh_o[(h2 * kDecMaxGroup + mg) * kD + md4]);
+      }
     }
-    __syncthreads();  // every read of sh_M / red above is done
-    red[part * kDecMaxGroup + gi] = L;
-  }
-  __syncthreads();
-  if (tid < kDecMaxGroup) {
-    float ll = 0.f;
-    for (int p2 = 0; p2 < kParts; ++p2) ll += red[p2 * kDecMaxGroup + tid];
-    sh_L[tid] = ll;
-  }
-  __syncthreads();
-  if (owner) {
-    // out = sum_s w_s o_s / L, kBatch independent 16-byte loads in flight per thread
-    constexpr int kBatch = 32;
-    const float* po = a.ws_o + (pbase + gq) * kD + d4;
-    const int64_t sstride = static_cast<int64_t>(kDecMaxGroup) * kD;
-    f32x4 acc = f32x4{};
-    for (int s0 = 0; s0 < a.n_splits; s0 += kBatch) {
-      f32x4 buf[kBatch];
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j)
-        buf[j] = (s0 + j < a.n_splits) ? *reinterpret_cast<const f32x4*>(po + (s0 + j) * sstride) : f32x4{};
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j)
-        if (s0 + j < a.n_splits) acc += wts[(s0 + j) * kDecMaxGroup + gq] * buf[j];
-    }
-    const float Lg = sh_L[gq];
-    const float inv = Lg > 0.f ? 1.f / Lg : 0.f;
-    uint16_t* o = a.out + static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(h * a.group + gq) * a.o_sh + d4;
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    uint16_t* out = a.out + static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(h * a.group + mg) * a.o_sh + md4;
     u32x2 pk;
-    pk[0] = pack_bf16x2(acc[0] * inv, acc[1] * inv);
-    pk[1] = pack_bf16x2(acc[2] * inv, acc[3] * inv);
-    *reinterpret_cast<u32x2*>(o) = pk;
+    pk[0] = pack_bf16x2(o[0] * inv, o[1] * inv);
+    pk[1] = pack_bf16x2(o[2] * inv, o[3] * inv);
+    *reinterpret_cast<u32x2*>(out) = pk;
   }
   if (tid == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

@@ -35,6 +35,12 @@ CASES = [
     ("qwen_g7_8192_k64", 8192, 28, 4, 1e7, 64.0, True),
     ("c1_g4_prerotated", 2048, 4, 1, 1e4, 2.0, False),
     ("narrow_window", 3000, 8, 2, 1e4, 0.3, True),
+    # GQA groups 1, 2 and 16: the split merge uses 8, 8 and 1 threads per (head, dims)
+    ("mha_g1", 5000, 4, 4, 1e4, 2.0, True),
+    ("g2_off", 3000, 8, 4, 1e4, None, True),
+    ("g16_k2", 6000, 16, 1, 5e5, 2.0, True),
+    # G = 16 with more splits than one merge batch (32) per thread
+    ("g16_long_off", 40000, 16, 1, 5e5, None, True),
 ]
 
 
