@@ -35,6 +35,23 @@ typedef __attribute__((address_space(3))) uint8_t lds_u8;
 constexpr float kLazyRescaleLog2 = 8.0f;
 constexpr float kLn2 = 0.6931471805599453f;
 
+// s_waitcnt immediate for vmcnt(0) alone (gfx9 encoding: vmcnt bits 3:0 and
+// 15:14, expcnt 6:4, lgkmcnt 11:8), issued through the builtin so the
+// compiler's own wait insertion accounts for it.
+constexpr int kWaitVm = 0x0F70;
+
+// Barrier inside the tile loop.  __syncthreads() carries a workgroup release
+// fence, for which the compiler waits until every pending global->LDS copy of
+// the wave has landed (vmcnt(0)) before the s_barrier; a copy requested at the
+// start of an MFMA phase would then stall the end of that same phase.  This
+// barrier waits only for the wave's LDS instructions (lgkmcnt(0): zero fills
+// written with ds_write); each copy is waited for explicitly (vmcnt(0)) by the
+// wave that issued it, before the barrier that precedes its first reader.  The
+// memory clobber keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void pf_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 __device__ __forceinline__ float pair_max(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
@@ -93,19 +110,36 @@ __device__ __forceinline__ bf16x8 lds_frag(const lds_u8* p) {
   return *reinterpret_cast<const __attribute__((address_space(3))) bf16x8*>(p);
 }
 
-// Stage one 64-key tile (4 pages) into LDS: waves 0-3 copy K (first L levels)
-// of page w, waves 4-7 copy V of page w-4.  Missing pages are zero-filled.
-__device__ __forceinline__ void pf_load_tile(const PrefillArgs& a, int b, int kvh, int t, int L,
-                                             lds_u8* stage, int wave, int lane) {
-  const int page = wave & 3;
-  const bool is_v = wave >= 4;
-  const int pidx = 4 * t + page;
+// Raw page-table entry of page `pidx` of sequence b (-1 past the keys), in a
+// vector register (every lane holds the same value).  Each wave fetches the
+// entry of its next page one tile ahead, so the table read is never waited for
+// at the start of a phase.  The load is kept a vector load on purpose: a scalar
+// load inside the tile loop shares the LDS wait counter and, since scalar loads
+// return out of order, would force every LDS wait behind it to drain fully.
+__device__ __forceinline__ int fetch_page(const PrefillArgs& a, int b, int pidx) {
+  int lane_zero;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(lane_zero));  // a value the compiler cannot prove uniform
   const int n_pages_k = (a.nk + kPage - 1) / kPage;
   int pg = -1;
-  if (pidx < n_pages_k) {
-    pg = a.page_table[static_cast<int64_t>(b) * a.max_pages + pidx];
-    if (pg < 0 || pg >= a.num_pages) pg = -1;
-  }
+  if (pidx < n_pages_k) pg = a.page_table[static_cast<int64_t>(b) * a.max_pages + pidx + lane_zero];
+  return pg;
+}
+
+// The wave-uniform page id of a fetched entry; -1 for an invalid entry.  Read
+// on every path before the register is fetched into again (otherwise the
+// compiler guards the refetch with a wait for every outstanding load).
+__device__ __forceinline__ int page_id(const PrefillArgs& a, int raw) {
+  const int pg = __builtin_amdgcn_readfirstlane(raw);
+  return (pg < 0 || pg >= a.num_pages) ? -1 : pg;
+}
+
+// Stage one 64-key tile (4 pages) into LDS: waves 0-3 copy K (first L levels)
+// of page w, waves 4-7 copy V of page w-4; `pg` is the page id (-1: missing
+// page, zero-filled).
+__device__ __forceinline__ void pf_load_tile(const PrefillArgs& a, int kvh, int pg, int L, lds_u8* stage,
+                                             int wave, int lane) {
+  const int page = wave & 3;
+  const bool is_v = wave >= 4;
   lds_u8* dst = stage + (is_v ? 4 * 4096 : 0) + page * 4096;
   if (pg < 0) {
     const u32x4 z = {0u, 0u, 0u, 0u};
@@ -290,7 +324,8 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
   int o_prev = 2 * kPfStageBytes, o_cur = 0, o_next = kPfStageBytes;
 
   // ---- prologue: stage tile 0 ----
-  if (T > 0) pf_load_tile(a, b, kvh, 0, w_ld.advance(a.lt, 0), smem + o_cur, wave, lane);
+  const int page_w = wave & 3;  // this wave's page within a tile
+  if (T > 0) pf_load_tile(a, kvh, page_id(a, fetch_page(a, b, page_w)), w_ld.advance(a.lt, 0), smem + o_cur, wave, lane);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (T > 0 && kPfTileN > a.nk) {  // zero V of keys past nk (0 * V must stay 0)
@@ -313,12 +348,23 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
   // (group 0: end of its softmax of t; group 1: end of its MFMA phase of t).
   // The MFMA phase runs unconditionally (P = 0 when there is nothing to add) so
   // the accumulators stay in place.
+  // next page-table entry of this wave: tile 1 for group 0, tile 2 for group 1
+  int pg_next;
   if (grp == 1) {
-    if (1 < T) pf_load_tile(a, b, kvh, 1, w_ld.advance(a.lt, 1), smem + o_next, wave, lane);
-    __syncthreads();  // group 1 starts one step late
+    if (1 < T)
+      pf_load_tile(a, kvh, page_id(a, fetch_page(a, b, 4 + page_w)), w_ld.advance(a.lt, 1), smem + o_next, wave,
+                   lane);
+    pg_next = fetch_page(a, b, 8 + page_w);
+    pf_barrier();  // group 1 starts one step late
+  } else {
+    pg_next = fetch_page(a, b, 4 + page_w);
   }
   for (int t = 0; t <= T; ++t) {
-    if (grp == 0 && t + 1 < T) pf_load_tile(a, b, kvh, t + 1, w_ld.advance(a.lt, t + 1), smem + o_next, wave, lane);
+    if (grp == 0) {
+      const int pg = page_id(a, pg_next);
+      if (t + 1 < T) pf_load_tile(a, kvh, pg, w_ld.advance(a.lt, t + 1), smem + o_next, wave, lane);
+      pg_next = fetch_page(a, b, 4 * (t + 2) + page_w);
+    }
     // ---- MFMA phase of tile t ----
 #ifndef ATF_PF_NO_PRIO
     __builtin_amdgcn_s_setprio(1);
@@ -355,9 +401,13 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
 #ifndef ATF_PF_NO_PRIO
     __builtin_amdgcn_s_setprio(0);
 #endif
-    if (grp == 1) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (grp == 1 && t + 2 < T) pf_load_tile(a, b, kvh, t + 2, w_ld.advance(a.lt, t + 2), smem + o_prev, wave, lane);
+    if (grp == 1) __builtin_amdgcn_s_waitcnt(kWaitVm);
+    pf_barrier();
+    if (grp == 1) {
+      const int pg = page_id(a, pg_next);
+      if (t + 2 < T) pf_load_tile(a, kvh, pg, w_ld.advance(a.lt, t + 2), smem + o_prev, wave, lane);
+      pg_next = fetch_page(a, b, 4 * (t + 3) + page_w);
+    }
     // ---- softmax phase of tile t (lane = query row) ----
     if (t < t_end) {
       const int n0 = t * kPfTileN;
@@ -416,8 +466,8 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
 #pragma unroll
       for (int i = 0; i < 4; ++i) Pf[i] = bf16x8{};
     }
-    if (grp == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+    if (grp == 0) __builtin_amdgcn_s_waitcnt(kWaitVm);
+    pf_barrier();
     // Tile t+1 has landed; group 0 zeroes the V of keys past nk in a partial
     // last tile (read no earlier than two barriers later).
     if (grp == 0 && t + 1 < T && (t + 1) * kPfTileN + kPfTileN > a.nk) {
