@@ -8,6 +8,9 @@
     cache           paged KV cache in the kernels' level-blocked layout
     ops             torch.library operators over the HIP C ABI
     interface       reference-shaped entry points (_flash_attn_fwd, decode)
+    model_tables    window and RoPE tables from a model config (rope scaling
+                    included) with the pair-order guard
+    hf              transformers attention-interface hook
 
 Importing the package does not load the HIP library; the first GPU call does,
 and fails loudly if it is missing.  The fp32 reference attention is test
@@ -15,11 +18,12 @@ infrastructure and lives outside the package (oracle/ at the repository root).
 """
 from . import atflash_window, fiwin_common, window_table
 
-__all__ = ["window_table", "atflash_window", "fiwin_common", "rope", "cache", "ops", "interface"]
+__all__ = ["window_table", "atflash_window", "fiwin_common", "rope", "cache", "ops", "interface", "model_tables",
+           "hf"]
 
 
 def __getattr__(name):
-    if name in ("rope", "cache", "ops", "interface"):
+    if name in ("rope", "cache", "ops", "interface", "model_tables", "hf"):
         import importlib
         return importlib.import_module(f".{name}", __name__)
     raise AttributeError(name)
