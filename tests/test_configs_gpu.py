@@ -1,0 +1,114 @@
+"""GPU parity at the benchmark configurations (long contexts, real shapes).
+
+C2  Llama-3.2-3B attention shape (24 q / 8 kv heads, RoPE base 5e5) prefill at
+    8K, 32K and 128K against the fp32 oracle on sampled 32-row tiles (window
+    k = 2; OFF at 32K).
+C3  Llama-3.2-3B decode: batch 8 at contexts up to 32K with ragged lengths and
+    randomly permuted pages, and batch 1 at 160K (k = 2 and OFF).
+C4  Qwen2.5-7B-1M shape (28 / 4 heads, base 1e7): prefill of 32K tokens in 8K
+    chunks against the growing paged cache equals the single-shot prefill bit
+    for bit; decode at 128K against the oracle (k = 2 and k = 64).
+"""
+import pytest
+import torch
+
+import helpers as H
+
+pytestmark = pytest.mark.gpu
+
+
+def _prefill(q, k, v, base, k_ret, dev):
+    from atflash import atflash_window as AW, interface, rope as R
+    N = k.shape[1]
+    zhi = None if k_ret is None else AW.window_zhi_from_kret(H.D, base, k_ret, 1 << 23)
+    rt = R.rope_table(N, R.inv_freq(H.D, base, dev))
+    out, _ = interface._flash_attn_fwd(q.to(dev), k.to(dev), v.to(dev), atflash_window_zhi=zhi, rope=rt)
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+@pytest.mark.parametrize("N,k_ret", [(8192, 2.0), (32768, 2.0), (32768, None), (131072, 2.0)])
+def test_c2_llama_prefill_sampled_tiles(N, k_ret, dev):
+    base, hq, hkv = 5e5, 24, 8
+    print(f"[C2] llama prefill N={N} k={k_ret}", flush=True)
+    q, k, v = H.qkv(1, N, hq, hkv, seed=N + 5)
+    out = _prefill(q, k, v, base, k_ret, dev)
+    rows = [0, 32 * 97, N // 2, N - 32]
+    kk = float("inf") if k_ret is None else k_ret
+    ref = H.prefill_oracle(q, k, v, base, kk, True, tile_rows=rows)
+    for r in rows:
+        mx, mean = H.assert_close(out[:, r:r + 32], ref[:, r:r + 32], f"N={N} rows {r}")
+        print(f"  rows {r}: max {mx:.3e} mean {mean:.3e}", flush=True)
+
+
+def _paged_decode(lens, hq, hkv, base, k_ret, dev, seed):
+    from atflash import atflash_window as AW, interface, rope as R
+    from atflash.cache import PagedKVCache
+    B = len(lens)
+    total_pages = sum(-(-n // 16) for n in lens) + 11
+    cache = PagedKVCache(total_pages, hkv, dev)
+    cache._free = torch.randperm(total_pages, generator=torch.Generator().manual_seed(seed)).tolist()
+    maxlen = max(lens)
+    rt = R.rope_table(maxlen, R.inv_freq(H.D, base, dev))
+    g = torch.Generator().manual_seed(seed + 1)
+    seqs = []
+    for b, n in enumerate(lens):
+        cache.add_sequence(b, n)
+        seqs.append((H.randn_bf16((1, n, hkv, H.D), g), H.randn_bf16((1, n, hkv, H.D), g)))
+    table = cache.page_table(list(range(B)))
+    for b, (k, v) in enumerate(seqs):
+        torch.ops.atflash.kv_write(cache.k, cache.v, k.to(dev), v.to(dev),
+                                   torch.zeros(1, dtype=torch.int32, device=dev), table[b:b + 1].contiguous(), rt, 0)
+    q = H.randn_bf16((B, hq, H.D), g)
+    seq_lens = torch.tensor(lens, dtype=torch.int32, device=dev)
+    zhi = None if k_ret is None else AW.window_zhi_from_kret(H.D, base, k_ret, 1 << 23)
+    out = interface.decode_paged(q.to(dev), cache, table, seq_lens, maxlen, zhi=zhi, rope=rt).cpu()
+    kk = float("inf") if k_ret is None else k_ret
+    for b, (k, v) in enumerate(seqs):
+        ref = H.decode_oracle(q[b], k[0], v[0], base, kk, True)
+        mx, mean = H.assert_close(out[b], ref, f"seq {b} len {lens[b]} k={k_ret}")
+        print(f"  seq {b} len {lens[b]}: max {mx:.3e} mean {mean:.3e}", flush=True)
+
+
+def test_c3_llama_decode_batch8_32k(dev):
+    print("[C3] llama decode batch 8 up to 32K, k=2", flush=True)
+    _paged_decode([32768, 31000, 20000, 16384, 9000, 4097, 1500, 33], 24, 8, 5e5, 2.0, dev, seed=31)
+
+
+@pytest.mark.parametrize("k_ret", [2.0, None])
+def test_c3_llama_decode_160k(k_ret, dev):
+    print(f"[C3] llama decode 160K k={k_ret}", flush=True)
+    _paged_decode([163840], 24, 8, 5e5, k_ret, dev, seed=33)
+
+
+@pytest.mark.parametrize("k_ret", [2.0, 64.0])
+def test_c4_qwen_decode_128k(k_ret, dev):
+    print(f"[C4] qwen decode 128K k={k_ret}", flush=True)
+    _paged_decode([131072], 28, 4, 1e7, k_ret, dev, seed=41)
+
+
+def test_c4_qwen_chunked_prefill_8k_chunks_bitwise(dev):
+    """32K tokens in 8K chunks (q_offset = 0, 8K, 16K, 24K) against the growing
+    paged cache, pages scattered over the pool, equals single shot bit for bit."""
+    from atflash import atflash_window as AW, interface, rope as R
+    from atflash.cache import PagedKVCache
+    base, N, hq, hkv, C = 1e7, 32768, 28, 4, 8192
+    print("[C4] qwen chunked prefill 32K in 8K chunks", flush=True)
+    q, k, v = H.qkv(1, N, hq, hkv, seed=43)
+    q, k, v = q.to(dev), k.to(dev), v.to(dev)
+    zhi = AW.window_zhi_from_kret(H.D, base, 2.0, 1 << 23)
+    rt = R.rope_table(N, R.inv_freq(H.D, base, dev))
+    single, _ = interface._flash_attn_fwd(q, k, v, atflash_window_zhi=zhi, rope=rt)
+    pool = N // 16 + 64
+    cache = PagedKVCache(pool, hkv, dev)
+    cache._free = torch.randperm(pool, generator=torch.Generator().manual_seed(4)).tolist()
+    cache.add_sequence(0, N)
+    table = cache.page_table([0])
+    outs = []
+    for c0 in range(0, N, C):
+        c1 = c0 + C
+        torch.ops.atflash.kv_write(cache.k, cache.v, k[:, c0:c1], v[:, c0:c1],
+                                   torch.tensor([c0], dtype=torch.int32, device=dev), table, rt, 0)
+        o, _ = interface.prefill_paged(q[:, c0:c1], cache, table, nk=c1, q_offset=c0, zhi=zhi, rope=rt)
+        outs.append(o)
+    assert torch.equal(torch.cat(outs, dim=1).cpu(), single.cpu())
