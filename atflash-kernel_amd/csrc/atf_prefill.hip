@@ -133,6 +133,49 @@ __device__ __forceinline__ int page_id(const PrefillArgs& a, int raw) {
   return (pg < 0 || pg >= a.num_pages) ? -1 : pg;
 }
 
+// LDS layout of a staged page.  An MFMA A operand is read with ds_read_b128,
+// lane l taking 16 bytes of row l%32 (half l/32 of the 16-element k slice).
+// The cache rows are 32 bytes long (16 keys of a V^T row, 16 dims of a K level
+// row), so reading them in place puts lanes j and j+4 of every 8-lane group on
+// the same LDS banks.  The staging copy therefore permutes the 16-byte chunks
+// of each 1 KB copy (its source address is per lane): LDS chunk i of a copy
+// holds half (i/16)%2 of K row i%16 of level i/32, resp. half i/32 of V^T row
+// i%32.  Every operand read is then 64 consecutive 16-byte chunks per half:
+//   K   level lv, token tk, half hf:  lv*512 + hf*256 + tk*16
+//   V^T row d (1 KB block d/32), half hf:  (d/32)*1024 + hf*512 + (d%32)*16
+__device__ __forceinline__ int k_copy_src(int lane) {
+  return ((lane >> 5) << 9) + ((lane & 15) << 5) + (((lane >> 4) & 1) << 4);
+}
+__device__ __forceinline__ int v_copy_src(int lane) { return ((lane & 31) << 5) + ((lane >> 5) << 4); }
+// Byte offset of V^T element (dim d, slot s) in a staged page.
+__device__ __forceinline__ int v_lds_elem(int d, int s) {
+  return ((d >> 5) << 10) + ((s >> 3) << 9) + ((d & 31) << 4) + ((s & 7) << 1);
+}
+
+// One direct global->LDS copy of 16 bytes per lane (a 1 KB row per wave) to
+// LDS address dst + 16 * lane, written as inline assembly.  When the compiler
+// sees a global->LDS copy anywhere in a loop, its wait insertion no longer
+// counts LDS reads in order and waits for all of them (lgkmcnt(0)) before
+// every use of one, which exposes the full LDS latency in front of each MFMA
+// of the operand ring.  The copies are therefore invisible to it: every copy
+// is waited for explicitly (vmcnt(0)) before the barrier that publishes it,
+// and a vector-load wait the compiler computes for its own loads only becomes
+// stricter when copies it does not count are in flight.  M0 holds the LDS
+// address for the copy (one wait state after it is written) and is restored.
+__device__ __forceinline__ void lds_copy16(const uint8_t* src, lds_u8* dst) {
+  const uint32_t la = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst)));
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(src), "s"(la)
+      : "memory");
+}
+
 // Stage one 64-key tile (4 pages) into LDS: waves 0-3 copy K (first L levels)
 // of page w, waves 4-7 copy V of page w-4; `pg` is the page id (-1: missing
 // page, zero-filled).
@@ -150,15 +193,14 @@ __device__ __forceinline__ void pf_load_tile(const PrefillArgs& a, int kvh, int 
   }
   const size_t blk = (static_cast<size_t>(pg) * a.hkv + kvh) * 4096;
   if (is_v) {
-    const uint8_t* src = reinterpret_cast<const uint8_t*>(a.v_cache) + blk;
+    const uint8_t* src = reinterpret_cast<const uint8_t*>(a.v_cache) + blk + v_copy_src(lane);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) __builtin_amdgcn_global_load_lds(src + i * 1024 + lane * 16, dst + i * 1024, 16, 0, 0);
+    for (int i = 0; i < 4; ++i) lds_copy16(src + i * 1024, dst + i * 1024);
   } else {
-    const uint8_t* src = reinterpret_cast<const uint8_t*>(a.k_cache) + blk;
+    const uint8_t* src = reinterpret_cast<const uint8_t*>(a.k_cache) + blk + k_copy_src(lane);
     const int npairs = (L + 1) >> 1;
     for (int lp = 0; lp < npairs; ++lp) {
-      if (lane < 32 || 2 * lp + 1 < L)
-        __builtin_amdgcn_global_load_lds(src + lp * 1024 + lane * 16, dst + lp * 1024, 16, 0, 0);
+      if (lane < 32 || 2 * lp + 1 < L) lds_copy16(src + lp * 1024, dst + lp * 1024);
     }
   }
 }
@@ -236,6 +278,60 @@ __device__ __forceinline__ void qk_tile(int L0, int L1, const lds_u8* k0, const 
   } else {
     S0 = qk_one(L0, k0, Qf, a0, C);
     S1 = qk_one(L1, k1, Qf, a1, C);
+  }
+}
+
+// The MFMA phase as one stream of MFMAs, each taking one 1 KB A operand from
+// LDS: stream i < 16 is PV step (ks, db) = (i/4, i%4), O[db] += V^T[db,ks] P^T[ks];
+// stream 16 + j is QK level j/2 of 32-key block j%2 (the first level starts
+// from C), 16 + 2L MFMAs in all when both blocks have L levels.  The operands
+// go through a ring of kRing registers: the read of operand i + kRing - 1 is
+// issued before MFMA i (scheduling barriers keep that order), so each read has
+// kRing - 1 MFMAs (32 cycles each) to arrive; the LDS latency under four SIMDs'
+// operand traffic is longer than one or two.  The PV part is shared by every
+// level count: it reads the first QK operands ahead in this order, which is
+// the same for any L (an operand past 2L is read and not used; its address is
+// still inside the staged tile).
+#ifndef ATF_PF_RING
+#define ATF_PF_RING 6
+#endif
+constexpr int kRing = ATF_PF_RING;
+static_assert(kRing >= 2 && kRing - 1 <= 16, "ring depth");
+
+__device__ __forceinline__ const lds_u8* stream_src(const lds_u8* vb, const lds_u8* kb, int i) {
+  if (i < 16) return vb + (i >> 2) * 4096 + (i & 3) * 1024;
+  const int j = i - 16;
+  return kb + (j & 1) * (2 * 4096) + (j >> 1) * 512;
+}
+
+__device__ __forceinline__ void pv_stream(const lds_u8* vb, const lds_u8* kb, const bf16x8 (&Pf)[4], f32x16 (&O)[4],
+                                          bf16x8 (&f)[kRing]) {
+#pragma unroll
+  for (int i = 0; i < kRing - 1; ++i) {
+    f[i] = lds_frag(stream_src(vb, kb, i));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    f[(i + kRing - 1) % kRing] = lds_frag(stream_src(vb, kb, i + kRing - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    O[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[i % kRing], Pf[i >> 2], O[i & 3], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+template <int L>
+__device__ __forceinline__ void qk_stream(const lds_u8* kb, bf16x8 (&f)[kRing], const u32x4 (&Qf)[kLevels],
+                                          const f32x16& C, f32x16 (&S)[2]) {
+  constexpr int NS = 16 + 2 * L;
+#pragma unroll
+  for (int i = 16; i < NS; ++i) {
+    if (i + kRing - 1 < NS) f[(i + kRing - 1) % kRing] = lds_frag(stream_src(kb, kb, i + kRing - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    const int j = i - 16;
+    S[j & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[i % kRing], __builtin_bit_cast(bf16x8, Qf[j >> 1]),
+                                                       (j >> 1) == 0 ? C : S[j & 1], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -330,11 +426,12 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
   __syncthreads();
   if (T > 0 && kPfTileN > a.nk) {  // zero V of keys past nk (0 * V must stay 0)
     const int page = threadIdx.x >> 7;
-    __attribute__((address_space(3))) uint16_t* vrow = reinterpret_cast<__attribute__((address_space(3))) uint16_t*>(
-        smem + o_cur + 4 * 4096 + page * 4096 + (threadIdx.x & 127) * 32);
+    const int d = threadIdx.x & 127;
+    lds_u8* vpage = smem + o_cur + 4 * 4096 + page * 4096;
 #pragma unroll
     for (int tk = 0; tk < kPage; ++tk)
-      if (page * kPage + tk >= a.nk) vrow[v_slot(tk)] = 0;
+      if (page * kPage + tk >= a.nk)
+        *reinterpret_cast<__attribute__((address_space(3))) uint16_t*>(vpage + v_lds_elem(d, v_slot(tk))) = 0;
     __syncthreads();
   }
 
@@ -370,33 +467,29 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
     __builtin_amdgcn_s_setprio(1);
 #endif
     {
-      const lds_u8* kbase = smem + o_cur + ((lane & 31) >> 4) * 4096 + (lane & 15) * 32 + (lane >> 5) * 16;
-      // O^T += V^T P^T for tile t-1 (P = 0 at t = 0); the operands of step ks+1
-      // (and finally the level-0 K operands of tile t) are read while step ks runs.
-      const lds_u8* vb = smem + (t == 0 ? o_cur : o_prev) + 4 * 4096 + (lane & 31) * 32 + (lane >> 5) * 16;
-      bf16x8 vf[4], vn[4], a0, a1;
-#pragma unroll
-      for (int db = 0; db < 4; ++db) vf[db] = lds_frag(vb + db * 1024);
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        if (ks < 3) {
-#pragma unroll
-          for (int db = 0; db < 4; ++db) vn[db] = lds_frag(vb + (ks + 1) * 4096 + db * 1024);
-        } else {
-          a0 = lds_frag(kbase);
-          a1 = lds_frag(kbase + 2 * 4096);
-        }
-#pragma unroll
-        for (int db = 0; db < 4; ++db) O[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db], Pf[ks], O[db], 0, 0, 0);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int db = 0; db < 4; ++db) vf[db] = vn[db];
-      }
-      // S^T = K Q^T over the surviving levels of each 32-key block of tile t
-      // (unused when the wave has no tile t).
+      const lds_u8* kbase = smem + o_cur + ((lane & 31) >> 4) * 4096 + (lane >> 5) * 256 + (lane & 15) * 16;
+      // O^T += V^T P^T for tile t-1 (P = 0 at t = 0), then S^T = K Q^T over the
+      // surviving levels of each 32-key block of tile t (unused when the wave
+      // has no tile t).
+      const lds_u8* vb = smem + (t == 0 ? o_cur : o_prev) + 4 * 4096 + (lane >> 5) * 512 + (lane & 31) * 16;
       const int L0 = w_far.advance(a.lt, t);
       const int L1 = w_near.advance(a.lt, t);
-      qk_tile(L0, L1, kbase, kbase + 2 * 4096, Qf, a0, a1, Cm, S[0], S[1]);
+      bf16x8 f[kRing];
+      pv_stream(vb, kbase, Pf, O, f);
+      if (L0 == L1) {
+        switch (L0) {
+          case 8: qk_stream<8>(kbase, f, Qf, Cm, S); break;
+          case 7: qk_stream<7>(kbase, f, Qf, Cm, S); break;
+          case 6: qk_stream<6>(kbase, f, Qf, Cm, S); break;
+          case 5: qk_stream<5>(kbase, f, Qf, Cm, S); break;
+          case 4: qk_stream<4>(kbase, f, Qf, Cm, S); break;
+          case 3: qk_stream<3>(kbase, f, Qf, Cm, S); break;
+          case 2: qk_stream<2>(kbase, f, Qf, Cm, S); break;
+          default: qk_stream<1>(kbase, f, Qf, Cm, S); break;
+        }
+      } else {  // a level boundary between the two blocks: two chains
+        qk_tile(L0, L1, kbase, kbase + 2 * 4096, Qf, f[16 % kRing], f[17 % kRing], Cm, S[0], S[1]);
+      }
     }
 #ifndef ATF_PF_NO_PRIO
     __builtin_amdgcn_s_setprio(0);
@@ -472,13 +565,14 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
     // last tile (read no earlier than two barriers later).
     if (grp == 0 && t + 1 < T && (t + 1) * kPfTileN + kPfTileN > a.nk) {
       const int n0 = (t + 1) * kPfTileN;
+      lds_u8* vpage = smem + o_next + 4 * 4096 + rank * 4096;
 #pragma unroll
       for (int rr = 0; rr < 2; ++rr) {
-        __attribute__((address_space(3))) uint16_t* vrow = reinterpret_cast<__attribute__((address_space(3))) uint16_t*>(
-            smem + o_next + 4 * 4096 + rank * 4096 + (lane * 2 + rr) * 32);
 #pragma unroll
         for (int tk = 0; tk < kPage; ++tk)
-          if (n0 + rank * kPage + tk >= a.nk) vrow[v_slot(tk)] = 0;
+          if (n0 + rank * kPage + tk >= a.nk)
+            *reinterpret_cast<__attribute__((address_space(3))) uint16_t*>(vpage + v_lds_elem(lane * 2 + rr, v_slot(tk))) =
+                0;
       }
     }
     // rotate the ring: tile t+1 becomes current

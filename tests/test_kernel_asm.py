@@ -12,7 +12,12 @@ silently and only show up as wrong numbers on the GPU:
   by a different VALU instruction fewer than 3 wait states later.
 
 These tests compile each kernel source to device assembly with the library's own
-flags and scan it for both.  The scanners are first run on small snippets in
+flags and scan it for both.  A third check guards a performance property: the
+prefill kernel's MFMA operand ring relies on the compiler counting LDS reads in
+issue order (``s_waitcnt lgkmcnt(N)`` with N > 0 before each MFMA).  A
+global->LDS copy that the compiler can see anywhere in the loop makes it wait
+for every outstanding LDS read (``lgkmcnt(0)``) instead, which still computes
+the right result but exposes the full LDS latency before each MFMA.  The scanners are first run on small snippets in
 which the mistake is planted, so a scanner that finds nothing is known to be
 able to find something.
 """
@@ -153,6 +158,41 @@ def test_dot_scanner_finds_an_early_read():
 
 # ------------------------------------------------------------ the kernels
 
+def lds_waits_before_mfma(asm, kernel):
+    """For each MFMA of `kernel`, the smallest lgkmcnt waited for since the
+    previous MFMA (None: no LDS wait)."""
+    start = asm.index(kernel + ":")
+    body = asm[start:asm.index("s_endpgm", start)]
+    out, cur = [], None
+    for _, s in _instructions(body):
+        m = re.match(r"s_waitcnt.*lgkmcnt\((\d+)\)", s)
+        if m:
+            cur = int(m.group(1)) if cur is None else min(cur, int(m.group(1)))
+        if s.startswith("v_mfma"):
+            out.append(cur)
+            cur = None
+    return out
+
+
+def longest_pipelined_run(waits, depth=3):
+    """Longest run of consecutive MFMAs waiting for at most all but `depth`
+    outstanding LDS reads (or none)."""
+    best = run = 0
+    for w in waits:
+        run = run + 1 if (w is None or w >= depth) else 0
+        best = max(best, run)
+    return best
+
+
+def test_wait_scanner_tells_pipelined_from_drained_reads():
+    mf = "v_mfma_f32_32x32x16_bf16 v[0:15], v[16:19], v[20:23], v[0:15]"
+    ring = "k:\n" + "".join(f"  ds_read_b128 v[{24 + 4 * (i % 6)}:{27 + 4 * (i % 6)}], v40\n"
+                             "  s_waitcnt lgkmcnt(5)\n  " + mf + "\n" for i in range(16)) + "  s_endpgm\n"
+    drained = ring.replace("lgkmcnt(5)", "lgkmcnt(0)")
+    assert longest_pipelined_run(lds_waits_before_mfma(ring, "k")) == 16
+    assert longest_pipelined_run(lds_waits_before_mfma(drained, "k")) == 0
+
+
 def _hipcc_or_skip():
     sys.path.insert(0, PKG)
     import build as B  # atflash-kernel_amd/build.py
@@ -197,3 +237,11 @@ def test_prefill_kernel_does_not_spill(kernel_asm):
     assert len(blocks) == 1, "prefill_kernel metadata not found"
     spill = re.search(r"\.vgpr_spill_count:\s+(\d+)", blocks[0])
     assert spill and int(spill.group(1)) == 0
+
+
+def test_prefill_operand_ring_keeps_lds_reads_in_flight(kernel_asm):
+    # the PV stream (16 MFMAs) and the 8-level QK stream each run with the
+    # operand reads of several later MFMAs still outstanding
+    waits = lds_waits_before_mfma(kernel_asm["atf_prefill.hip"], "_ZN3atf14prefill_kernelENS_11PrefillArgsE")
+    assert len(waits) >= 32
+    assert longest_pipelined_run(waits) >= 15, waits
