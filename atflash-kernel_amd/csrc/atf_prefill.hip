@@ -197,11 +197,11 @@ __device__ __forceinline__ void pf_load_tile(const PrefillArgs& a, int kvh, int 
 #pragma unroll
     for (int i = 0; i < 4; ++i) lds_copy16(src + i * 1024, dst + i * 1024);
   } else {
+    // whole 1 KB level pairs (an odd L also copies level L, which is not read)
     const uint8_t* src = reinterpret_cast<const uint8_t*>(a.k_cache) + blk + k_copy_src(lane);
-    const int npairs = (L + 1) >> 1;
-    for (int lp = 0; lp < npairs; ++lp) {
-      if (lane < 32 || 2 * lp + 1 < L) lds_copy16(src + lp * 1024, dst + lp * 1024);
-    }
+#pragma unroll
+    for (int lp = 0; lp < kLevels / 2; ++lp)
+      if (2 * lp < L) lds_copy16(src + lp * 1024, dst + lp * 1024);
   }
 }
 
@@ -304,13 +304,18 @@ __device__ __forceinline__ const lds_u8* stream_src(const lds_u8* vb, const lds_
   return kb + (j & 1) * (2 * 4096) + (j >> 1) * 512;
 }
 
-__device__ __forceinline__ void pv_stream(const lds_u8* vb, const lds_u8* kb, const bf16x8 (&Pf)[4], f32x16 (&O)[4],
-                                          bf16x8 (&f)[kRing]) {
+// The first kRing - 1 operands of the stream (V^T only).
+static_assert(kRing - 1 <= 16, "ring prefetch must stay within the PV operands");
+__device__ __forceinline__ void pv_prefetch(const lds_u8* vb, bf16x8 (&f)[kRing]) {
 #pragma unroll
   for (int i = 0; i < kRing - 1; ++i) {
-    f[i] = lds_frag(stream_src(vb, kb, i));
+    f[i] = lds_frag(stream_src(vb, vb, i));
     __builtin_amdgcn_sched_barrier(0);
   }
+}
+
+__device__ __forceinline__ void pv_stream(const lds_u8* vb, const lds_u8* kb, const bf16x8 (&Pf)[4], f32x16 (&O)[4],
+                                          bf16x8 (&f)[kRing]) {
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     f[(i + kRing - 1) % kRing] = lds_frag(stream_src(vb, kb, i + kRing - 1));
@@ -445,6 +450,7 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
   // (group 0: end of its softmax of t; group 1: end of its MFMA phase of t).
   // The MFMA phase runs unconditionally (P = 0 when there is nothing to add) so
   // the accumulators stay in place.
+  const int v_lane = 4 * 4096 + (lane >> 5) * 512 + (lane & 31) * 16;
   // next page-table entry of this wave: tile 1 for group 0, tile 2 for group 1
   int pg_next;
   if (grp == 1) {
@@ -471,10 +477,11 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
       // O^T += V^T P^T for tile t-1 (P = 0 at t = 0), then S^T = K Q^T over the
       // surviving levels of each 32-key block of tile t (unused when the wave
       // has no tile t).
-      const lds_u8* vb = smem + (t == 0 ? o_cur : o_prev) + 4 * 4096 + (lane >> 5) * 512 + (lane & 31) * 16;
+      const lds_u8* vb = smem + (t == 0 ? o_cur : o_prev) + v_lane;
       const int L0 = w_far.advance(a.lt, t);
       const int L1 = w_near.advance(a.lt, t);
       bf16x8 f[kRing];
+      pv_prefetch(vb, f);
       pv_stream(vb, kbase, Pf, O, f);
       if (L0 == L1) {
         switch (L0) {
@@ -505,19 +512,21 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
     if (t < t_end) {
       const int n0 = t * kPfTileN;
       const bool need_mask = (n0 + kPfTileN - 1 > pos0) || (n0 + kPfTileN > a.nk);
-      const int row_pos = pos0 + (lane & 31);
+      if (need_mask) {
+        // element (kb, r) holds key n0 + 4*(lane/32) + c with c = 32kb + 8(r/4) + r%4;
+        // masked when key > min(row position, nk - 1).  Selects, no branches.
+        const int thr = min(pos0 + (lane & 31), a.nk - 1) - n0 - 4 * (lane >> 5);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            S[kb][r] = (32 * kb + 8 * (r >> 2) + (r & 3) > thr) ? NEG_INF : S[kb][r];
+      }
       float mx = NEG_INF;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          if (need_mask) {
-            const int key = n0 + 32 * kb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            if (key > row_pos || key >= a.nk) S[kb][r] = NEG_INF;
-          }
-          mx = fmaxf(mx, S[kb][r]);
-        }
-      }
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, S[kb][r]);
       mx = pair_max(mx);
       // S already holds score - m_ref.  On the first tile (key 0 is visible to
       // every row, so mx is finite) and wherever the max grew past m_ref by more
