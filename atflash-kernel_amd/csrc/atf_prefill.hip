@@ -42,8 +42,8 @@ constexpr int kWaitVm = 0x0F70;
 
 // Barrier inside the tile loop.  __syncthreads() carries a workgroup release
 // fence, for which the compiler waits until every pending global->LDS copy of
-// the wave has landed (vmcnt(0)) before the s_barrier; a copy requested at the
-// start of an MFMA phase would then stall the end of that same phase.  This
+// the wave has landed (vmcnt(0)) before the s_barrier; a copy requested during
+// a phase would then stall the barrier that ends that same phase.  This
 // barrier waits only for the wave's LDS instructions (lgkmcnt(0): zero fills
 // written with ds_write); each copy is waited for explicitly (vmcnt(0)) by the
 // wave that issued it, before the barrier that precedes its first reader.  The
@@ -445,11 +445,14 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
 #pragma unroll
   for (int i = 0; i < 4; ++i) Pf[i] = bf16x8{};
   // Global step k: group g runs phase k - g.  Phase 2t is the MFMA phase of
-  // tile t (PV of tile t-1, QK of tile t), phase 2t+1 its softmax.  Tile t+1 is
-  // requested at step 2t and has landed after the barrier ending step 2t+1
-  // (group 0: end of its softmax of t; group 1: end of its MFMA phase of t).
-  // The MFMA phase runs unconditionally (P = 0 when there is nothing to add) so
-  // the accumulators stay in place.
+  // tile t (PV of tile t-1, QK of tile t), phase 2t+1 its softmax.  Copies are
+  // issued in softmax phases only, so an MFMA phase never waits behind them:
+  // K of tile t+2 by group 0 in its softmax of tile t (step 2t+1), V of tile
+  // t+2 by group 1 in its softmax of tile t (step 2t+2).  Each wave waits for
+  // its copies before the barrier ending its next MFMA phase (steps 2t+2 and
+  // 2t+3); tile t+2 is first read at step 2t+4.  Tile 1 is requested before
+  // the loop.  The MFMA phase runs unconditionally (P = 0 when there is
+  // nothing to add) so the accumulators stay in place.
   const int v_lane = 4 * 4096 + (lane >> 5) * 512 + (lane & 31) * 16;
   // next page-table entry of this wave: tile 1 for group 0, tile 2 for group 1
   int pg_next;
@@ -460,14 +463,12 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
     pg_next = fetch_page(a, b, 8 + page_w);
     pf_barrier();  // group 1 starts one step late
   } else {
-    pg_next = fetch_page(a, b, 4 + page_w);
+    if (1 < T)
+      pf_load_tile(a, kvh, page_id(a, fetch_page(a, b, 4 + page_w)), w_ld.advance(a.lt, 1), smem + o_next, wave,
+                   lane);
+    pg_next = fetch_page(a, b, 8 + page_w);
   }
   for (int t = 0; t <= T; ++t) {
-    if (grp == 0) {
-      const int pg = page_id(a, pg_next);
-      if (t + 1 < T) pf_load_tile(a, kvh, pg, w_ld.advance(a.lt, t + 1), smem + o_next, wave, lane);
-      pg_next = fetch_page(a, b, 4 * (t + 2) + page_w);
-    }
     // ---- MFMA phase of tile t ----
 #ifndef ATF_PF_NO_PRIO
     __builtin_amdgcn_s_setprio(1);
@@ -501,9 +502,14 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
 #ifndef ATF_PF_NO_PRIO
     __builtin_amdgcn_s_setprio(0);
 #endif
-    if (grp == 1) __builtin_amdgcn_s_waitcnt(kWaitVm);
+    // this wave's copies of tile t+1 (requested in its previous phase) land
+    // before the barrier after which tile t+1 is first read
+    __builtin_amdgcn_s_waitcnt(kWaitVm);
     pf_barrier();
-    if (grp == 1) {
+    {
+      // K (group 0) or V (group 1) of tile t+2 into the stage of tile t-1:
+      // both groups have read that tile's K, and its V is read only by the
+      // MFMA phases of tile t, which end before the copy into V starts
       const int pg = page_id(a, pg_next);
       if (t + 2 < T) pf_load_tile(a, kvh, pg, w_ld.advance(a.lt, t + 2), smem + o_prev, wave, lane);
       pg_next = fetch_page(a, b, 4 * (t + 3) + page_w);
@@ -568,7 +574,6 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
 #pragma unroll
       for (int i = 0; i < 4; ++i) Pf[i] = bf16x8{};
     }
-    if (grp == 0) __builtin_amdgcn_s_waitcnt(kWaitVm);
     pf_barrier();
     // Tile t+1 has landed; group 0 zeroes the V of keys past nk in a partial
     // last tile (read no earlier than two barriers later).
