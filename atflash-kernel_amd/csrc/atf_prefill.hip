@@ -152,8 +152,8 @@ __device__ __forceinline__ int v_lds_elem(int d, int s) {
   return ((d >> 5) << 10) + ((s >> 3) << 9) + ((d & 31) << 4) + ((s & 7) << 1);
 }
 
-// One direct global->LDS copy of 16 bytes per lane (a 1 KB row per wave) to
-// LDS address dst + 16 * lane, written as inline assembly.  When the compiler
+// Direct global->LDS copies (16 bytes per lane, a 1 KB row per wave, to LDS
+// address dst + 16 * lane), written as inline assembly.  When the compiler
 // sees a global->LDS copy anywhere in a loop, its wait insertion no longer
 // counts LDS reads in order and waits for all of them (lgkmcnt(0)) before
 // every use of one, which exposes the full LDS latency in front of each MFMA
@@ -161,26 +161,44 @@ __device__ __forceinline__ int v_lds_elem(int d, int s) {
 // is waited for explicitly (vmcnt(0)) before the barrier that publishes it,
 // and a vector-load wait the compiler computes for its own loads only becomes
 // stricter when copies it does not count are in flight.  M0 holds the LDS
-// address for the copy (one wait state after it is written) and is restored.
-__device__ __forceinline__ void lds_copy16(const uint8_t* src, lds_u8* dst) {
+// address for the copies (one wait state after it is written) and is restored.
+//
+// lds_copy_rows<N> copies N consecutive 1 KB rows: lane l reads 16 bytes at
+// base + voff(l) + 1024 i (a wave-uniform base in scalar registers plus a
+// per-lane offset) and writes LDS dst + 16 l + 1024 i.  The instruction's
+// immediate offset moves the global and the LDS address alike, so one M0
+// setting serves all N rows.
+template <int N>
+__device__ __forceinline__ void lds_copy_rows(const uint8_t* base, uint32_t voff, lds_u8* dst) {
+  static_assert(N >= 1 && N <= 4, "1 to 4 rows");
   const uint32_t la = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst)));
   uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %2\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, off\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "v"(src), "s"(la)
-      : "memory");
+#define ATF_LDS_ROW(off) "global_load_lds_dwordx4 %1, %2 offset:" #off "\n\t"
+  if constexpr (N == 1)
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t" ATF_LDS_ROW(0) "s_mov_b32 m0, %0"
+                 : "=&s"(saved) : "v"(voff), "s"(base), "s"(la) : "memory");
+  else if constexpr (N == 2)
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t" ATF_LDS_ROW(0) ATF_LDS_ROW(1024)
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(saved) : "v"(voff), "s"(base), "s"(la) : "memory");
+  else if constexpr (N == 3)
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t" ATF_LDS_ROW(0) ATF_LDS_ROW(1024)
+                 ATF_LDS_ROW(2048) "s_mov_b32 m0, %0"
+                 : "=&s"(saved) : "v"(voff), "s"(base), "s"(la) : "memory");
+  else
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t" ATF_LDS_ROW(0) ATF_LDS_ROW(1024)
+                 ATF_LDS_ROW(2048) ATF_LDS_ROW(3072) "s_mov_b32 m0, %0"
+                 : "=&s"(saved) : "v"(voff), "s"(base), "s"(la) : "memory");
+#undef ATF_LDS_ROW
 }
 
 // Stage one 64-key tile (4 pages) into LDS: waves 0-3 copy K (first L levels)
 // of page w, waves 4-7 copy V of page w-4; `pg` is the page id (-1: missing
 // page, zero-filled).
+// `voff` is the lane's chunk offset within a copied 1 KB row (k_copy_src or
+// v_copy_src for the wave's half).
 __device__ __forceinline__ void pf_load_tile(const PrefillArgs& a, int kvh, int pg, int L, lds_u8* stage,
-                                             int wave, int lane) {
+                                             int wave, int lane, uint32_t voff) {
   const int page = wave & 3;
   const bool is_v = wave >= 4;
   lds_u8* dst = stage + (is_v ? 4 * 4096 : 0) + page * 4096;
@@ -193,15 +211,16 @@ __device__ __forceinline__ void pf_load_tile(const PrefillArgs& a, int kvh, int 
   }
   const size_t blk = (static_cast<size_t>(pg) * a.hkv + kvh) * 4096;
   if (is_v) {
-    const uint8_t* src = reinterpret_cast<const uint8_t*>(a.v_cache) + blk + v_copy_src(lane);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) lds_copy16(src + i * 1024, dst + i * 1024);
+    lds_copy_rows<4>(reinterpret_cast<const uint8_t*>(a.v_cache) + blk, voff, dst);
   } else {
     // whole 1 KB level pairs (an odd L also copies level L, which is not read)
-    const uint8_t* src = reinterpret_cast<const uint8_t*>(a.k_cache) + blk + k_copy_src(lane);
-#pragma unroll
-    for (int lp = 0; lp < kLevels / 2; ++lp)
-      if (2 * lp < L) lds_copy16(src + lp * 1024, dst + lp * 1024);
+    const uint8_t* src = reinterpret_cast<const uint8_t*>(a.k_cache) + blk;
+    switch ((L + 1) >> 1) {
+      case 4: lds_copy_rows<4>(src, voff, dst); break;
+      case 3: lds_copy_rows<3>(src, voff, dst); break;
+      case 2: lds_copy_rows<2>(src, voff, dst); break;
+      default: lds_copy_rows<1>(src, voff, dst); break;
+    }
   }
 }
 
@@ -426,7 +445,8 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
 
   // ---- prologue: stage tile 0 ----
   const int page_w = wave & 3;  // this wave's page within a tile
-  if (T > 0) pf_load_tile(a, kvh, page_id(a, fetch_page(a, b, page_w)), w_ld.advance(a.lt, 0), smem + o_cur, wave, lane);
+  const uint32_t copy_off = static_cast<uint32_t>(wave >= 4 ? v_copy_src(lane) : k_copy_src(lane));
+  if (T > 0) pf_load_tile(a, kvh, page_id(a, fetch_page(a, b, page_w)), w_ld.advance(a.lt, 0), smem + o_cur, wave, lane, copy_off);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (T > 0 && kPfTileN > a.nk) {  // zero V of keys past nk (0 * V must stay 0)
@@ -459,13 +479,13 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
   if (grp == 1) {
     if (1 < T)
       pf_load_tile(a, kvh, page_id(a, fetch_page(a, b, 4 + page_w)), w_ld.advance(a.lt, 1), smem + o_next, wave,
-                   lane);
+                   lane, copy_off);
     pg_next = fetch_page(a, b, 8 + page_w);
     pf_barrier();  // group 1 starts one step late
   } else {
     if (1 < T)
       pf_load_tile(a, kvh, page_id(a, fetch_page(a, b, 4 + page_w)), w_ld.advance(a.lt, 1), smem + o_next, wave,
-                   lane);
+                   lane, copy_off);
     pg_next = fetch_page(a, b, 8 + page_w);
   }
   for (int t = 0; t <= T; ++t) {
@@ -511,7 +531,7 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
       // both groups have read that tile's K, and its V is read only by the
       // MFMA phases of tile t, which end before the copy into V starts
       const int pg = page_id(a, pg_next);
-      if (t + 2 < T) pf_load_tile(a, kvh, pg, w_ld.advance(a.lt, t + 2), smem + o_prev, wave, lane);
+      if (t + 2 < T) pf_load_tile(a, kvh, pg, w_ld.advance(a.lt, t + 2), smem + o_prev, wave, lane, copy_off);
       pg_next = fetch_page(a, b, 4 * (t + 3) + page_w);
     }
     // ---- softmax phase of tile t (lane = query row) ----
