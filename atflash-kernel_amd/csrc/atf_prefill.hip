@@ -61,25 +61,6 @@ __device__ __forceinline__ float pair_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// acc + x.lo + x.hi for a packed bf16 pair (row sums of the bf16 P used in PV).
-// Written as the VOP3P instruction: the clang builtin for the bf16 dot2 lowers
-// to the VOP2 form with the same source register for every element of a
-// vector (ROCm 7.2), which sums the wrong values.
-//
-// The dot instruction writes its result through the dot pipeline: a following
-// dot of the same opcode may take it as its accumulator at once, but any other
-// VALU read needs 3 wait states, which the compiler cannot insert for inline
-// asm.  The last link of each tile's chain therefore carries its own wait
-// states inside the same statement (nothing can be scheduled in between).
-__device__ __forceinline__ float dot2_ones(uint32_t x, float acc) {
-  asm("v_dot2_f32_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(x), "v"(0x3f803f80u));
-  return acc;
-}
-__device__ __forceinline__ float dot2_ones_last(uint32_t x, float acc) {
-  asm("v_dot2_f32_bf16 %0, %1, %2, %0\n\ts_nop 4" : "+v"(acc) : "v"(x), "v"(0x3f803f80u));
-  return acc;
-}
-
 // Level count of tile t for a fixed (query anchor, key offset) pair as t walks
 // up: level i is read from tile T_i = ceil((anchor - off - zhi[i]) / 64) on, so
 // L(t) = #{i : T_i <= t} (the D_eff rule at distance anchor - (64 t + off)).
@@ -585,7 +566,7 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
             const float p0 = fast_exp2(S[kb][8 * hs + 2 * i]);
             const float p1 = fast_exp2(S[kb][8 * hs + 2 * i + 1]);
             pk[i] = pack_bf16x2(p0, p1);
-            l_run = (kb == 1 && hs == 1 && i == 3) ? dot2_ones_last(pk[i], l_run) : dot2_ones(pk[i], l_run);
+            l_run += p0 + p1;
           }
           Pf[2 * kb + hs] = __builtin_bit_cast(bf16x8, pk);
         }

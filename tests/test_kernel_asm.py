@@ -1,9 +1,9 @@
 """CPU checks on the gfx950 assembly of the HIP kernels.
 
-The prefill kernel issues some instructions through inline asm (LDS operand
-reads with explicit waits, the bf16 dot2 row sums).  The compiler schedules
-around inline asm without knowing its latencies, so two mistakes compile
-silently and only show up as wrong numbers on the GPU:
+Instructions issued through inline asm (LDS operand reads with explicit waits,
+the bf16 dot2 instruction) are scheduled by the compiler without knowing their
+latencies, so two mistakes compile silently and only show up as wrong numbers
+on the GPU:
 
 * a register written by an inline ``ds_read`` is read, copied or overwritten
   before the ``s_waitcnt lgkmcnt`` that covers the read (the copy sees stale
