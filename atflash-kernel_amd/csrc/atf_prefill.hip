@@ -340,6 +340,28 @@ __device__ __forceinline__ void qk_stream(const lds_u8* kb, bf16x8 (&f)[kRing], 
   }
 }
 
+// P = exp2(S) of a tile packed to bf16 (the B operands of the next PV steps),
+// and the lane's partial row sum of P.
+__device__ __forceinline__ float exp_tile(const f32x16 (&S)[2], bf16x8 (&Pf)[4]) {
+  float lt = 0.f;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+    for (int hs = 0; hs < 2; ++hs) {
+      u32x4 pk;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p0 = fast_exp2(S[kb][8 * hs + 2 * i]);
+        const float p1 = fast_exp2(S[kb][8 * hs + 2 * i + 1]);
+        pk[i] = pack_bf16x2(p0, p1);
+        lt += p0 + p1;
+      }
+      Pf[2 * kb + hs] = __builtin_bit_cast(bf16x8, pk);
+    }
+  }
+  return lt;
+}
+
 __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
   lds_u8* smem = (lds_u8*)(smem_raw);
@@ -529,48 +551,41 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
           for (int r = 0; r < 16; ++r)
             S[kb][r] = (32 * kb + 8 * (r >> 2) + (r & 3) > thr) ? NEG_INF : S[kb][r];
       }
-      float mx = NEG_INF;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, S[kb][r]);
-      mx = pair_max(mx);
-      // S already holds score - m_ref.  On the first tile (key 0 is visible to
-      // every row, so mx is finite) and wherever the max grew past m_ref by more
-      // than 8, m_ref moves up to the max: O and l are rescaled and this tile's
-      // scores shifted by the same delta (0 for the other lanes of the wave).
-      const bool grow = (t == 0) || mx > kLazyRescaleLog2;
-      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-        const float delta = grow ? mx : 0.f;
-        if (t > 0) {
-          const float alpha = fast_exp2(-delta);
-          l_run *= alpha;
-#pragma unroll
-          for (int db = 0; db < 4; ++db) O[db] *= alpha;
-        }
-        m_ref += delta;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) Cm[i] = -m_ref;
+      // S holds score - m_ref, so every P = exp2(S) is at most 256 unless a
+      // score exceeds m_ref by more than 8; P >= 0, so that shows as a partial
+      // row sum above 256 (or an infinite one).  Only then, and on the first
+      // tile (key 0 is visible to every row, so its max is finite), is the row
+      // max taken: where it exceeds m_ref by more than 8 (always on the first
+      // tile), m_ref moves up to it, O and l are rescaled, and the tile's P is
+      // computed again from the shifted scores (shift 0 for the other lanes).
+      float lt = exp_tile(S, Pf);
+      if (__builtin_amdgcn_ballot_w64((t == 0) || !(lt <= 256.f)) != 0) {
+        float mx = NEG_INF;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) S[kb][r] -= delta;
-      }
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, S[kb][r]);
+        mx = pair_max(mx);
+        const bool grow = (t == 0) || mx > kLazyRescaleLog2;
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+          const float delta = grow ? mx : 0.f;
+          if (t > 0) {
+            const float alpha = fast_exp2(-delta);
+            l_run *= alpha;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int hs = 0; hs < 2; ++hs) {
-          u32x4 pk;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float p0 = fast_exp2(S[kb][8 * hs + 2 * i]);
-            const float p1 = fast_exp2(S[kb][8 * hs + 2 * i + 1]);
-            pk[i] = pack_bf16x2(p0, p1);
-            l_run += p0 + p1;
+            for (int db = 0; db < 4; ++db) O[db] *= alpha;
           }
-          Pf[2 * kb + hs] = __builtin_bit_cast(bf16x8, pk);
+          m_ref += delta;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) Cm[i] = -m_ref;
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) S[kb][r] -= delta;
+          lt = exp_tile(S, Pf);
         }
       }
+      l_run += lt;
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i) Pf[i] = bf16x8{};
