@@ -50,11 +50,31 @@ struct PageRegs {
   int n0;
 };
 
-__device__ __forceinline__ void dec_load_page(const DecodeArgs& a, int b, int h, int p, int N, int lane,
+// Page-table entries of the kDecUnroll pages starting at p0, in vector
+// registers (every lane holds the same value), -1 for pages at or past p_end.
+// The loads are unconditional (the index is clamped into [p_begin, p_end)) and
+// the past-the-end entries are selected afterwards: a load guarded by a branch
+// with a default value makes the compiler wait for every outstanding load
+// before the register's next use.  A wave fetches the entries of its next
+// group while it computes the current one, so the K/V loads of a group are
+// issued back to back without waiting for the table.
+__device__ __forceinline__ void dec_fetch_group(const DecodeArgs& a, int b, int p0, int p_begin, int p_end,
+                                                int (&e)[kDecUnroll]) {
+  const int* row = a.page_table + static_cast<int64_t>(b) * a.max_pages;
+#pragma unroll
+  for (int u = 0; u < kDecUnroll; ++u) {
+    const int p = p0 + u;
+    const int v = row[max(p_begin, min(p, p_end - 1))];
+    e[u] = (p < p_end) ? v : -1;
+  }
+}
+
+// K and V operands of page p whose page-table entry is `raw`.
+__device__ __forceinline__ void dec_load_page(const DecodeArgs& a, int h, int raw, int p, int N, int lane,
                                               PageRegs& r) {
   r.n0 = p * kPage;
   r.L = levels_of(a.lt, max(0, (N - 1) - (r.n0 + kPage - 1)));
-  int pg = a.page_table[static_cast<int64_t>(b) * a.max_pages + p];
+  const int pg = __builtin_amdgcn_readfirstlane(raw);
   const bool ok = pg >= 0 && pg < a.num_pages;
   const size_t blk = (static_cast<size_t>(ok ? pg : 0) * a.hkv + h) * kBlockElems;
   const uint16_t* kb = a.k_cache + blk;
@@ -134,12 +154,17 @@ void decode_kernel(DecodeArgs a) {
   float m_run = NEG_INF, l_run = 0.f;
 
   // wave w takes the groups of kDecUnroll pages that start at p_begin + kDecUnroll * (w + kDecWaves * i)
-  for (int p0 = p_begin + kDecUnroll * wave; p0 < p_end; p0 += kDecUnroll * kDecWaves) {
+  constexpr int kStride = kDecUnroll * kDecWaves;
+  int ent[kDecUnroll];
+  const int p_first = p_begin + kDecUnroll * __builtin_amdgcn_readfirstlane(wave);
+  if (p_first < p_end) dec_fetch_group(a, b, p_first, p_begin, p_end, ent);
+  for (int p0 = p_first; p0 < p_end; p0 += kStride) {
     PageRegs pr[kDecUnroll];
 #pragma unroll
     for (int u = 0; u < kDecUnroll; ++u) {
-      if (p0 + u < p_end) dec_load_page(a, b, h, p0 + u, N, lane, pr[u]);
+      if (p0 + u < p_end) dec_load_page(a, h, ent[u], p0 + u, N, lane, pr[u]);
     }
+    dec_fetch_group(a, b, p0 + kStride, p_begin, p_end, ent);
 #pragma unroll
     for (int u = 0; u < kDecUnroll; ++u) {
       if (p0 + u >= p_end) break;
