@@ -5,9 +5,10 @@ C2  Llama-3.2-3B attention shape (24 q / 8 kv heads, RoPE base 5e5) prefill at
     k = 2; OFF at 32K).
 C3  Llama-3.2-3B decode: batch 8 at contexts up to 32K with ragged lengths and
     randomly permuted pages, and batch 1 at 160K (k = 2 and OFF).
-C4  Qwen2.5-7B-1M shape (28 / 4 heads, base 1e7): prefill of 32K tokens in 8K
-    chunks against the growing paged cache equals the single-shot prefill bit
-    for bit; decode at 128K against the oracle (k = 2 and k = 64).
+C4  Qwen2.5-7B-1M shape (28 / 4 heads, base 1e7): prefill of 32K and of 512K
+    tokens in 8K chunks against the growing paged cache equals the single-shot
+    prefill bit for bit; decode at 128K (k = 2 and k = 64) and at 512K (k = 2)
+    against the oracle.
 """
 import pytest
 import torch
@@ -87,15 +88,30 @@ def test_c4_qwen_decode_128k(k_ret, dev):
     _paged_decode([131072], 28, 4, 1e7, k_ret, dev, seed=41)
 
 
-def test_c4_qwen_chunked_prefill_8k_chunks_bitwise(dev):
-    """32K tokens in 8K chunks (q_offset = 0, 8K, 16K, 24K) against the growing
+def test_c4_qwen_decode_512k(dev):
+    print("[C4] qwen decode 512K k=2", flush=True)
+    _paged_decode([524288], 28, 4, 1e7, 2.0, dev, seed=45)
+
+
+def _gpu_qkv(N, hq, hkv, dev, seed):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    return tuple(torch.randn((1, N, h, H.D), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+                 for h in (hq, hkv, hkv))
+
+
+@pytest.mark.parametrize("N", [32768, 524288])
+def test_c4_qwen_chunked_prefill_8k_chunks_bitwise(N, dev):
+    """N tokens in 8K chunks (q_offset = 0, 8K, 16K, ...) against the growing
     paged cache, pages scattered over the pool, equals single shot bit for bit."""
     from atflash import atflash_window as AW, interface, rope as R
     from atflash.cache import PagedKVCache
-    base, N, hq, hkv, C = 1e7, 32768, 28, 4, 8192
-    print("[C4] qwen chunked prefill 32K in 8K chunks", flush=True)
-    q, k, v = H.qkv(1, N, hq, hkv, seed=43)
-    q, k, v = q.to(dev), k.to(dev), v.to(dev)
+    base, hq, hkv, C = 1e7, 28, 4, 8192
+    print(f"[C4] qwen chunked prefill {N} in 8K chunks", flush=True)
+    if N <= 32768:
+        q, k, v = H.qkv(1, N, hq, hkv, seed=43)
+        q, k, v = q.to(dev), k.to(dev), v.to(dev)
+    else:
+        q, k, v = _gpu_qkv(N, hq, hkv, dev, seed=47)
     zhi = AW.window_zhi_from_kret(H.D, base, 2.0, 1 << 23)
     rt = R.rope_table(N, R.inv_freq(H.D, base, dev))
     single, _ = interface._flash_attn_fwd(q, k, v, atflash_window_zhi=zhi, rope=rt)
@@ -111,4 +127,4 @@ def test_c4_qwen_chunked_prefill_8k_chunks_bitwise(dev):
                                    torch.tensor([c0], dtype=torch.int32, device=dev), table, rt, 0)
         o, _ = interface.prefill_paged(q[:, c0:c1], cache, table, nk=c1, q_offset=c0, zhi=zhi, rope=rt)
         outs.append(o)
-    assert torch.equal(torch.cat(outs, dim=1).cpu(), single.cpu())
+    assert torch.equal(torch.cat(outs, dim=1), single)
