@@ -122,6 +122,23 @@ void decode_kernel(DecodeArgs a) {
   const float NEG_INF = -__builtin_huge_valf();
   const float c = a.scale_log2;
 
+  // wave w takes the groups of kDecUnroll pages that start at p_begin + kDecUnroll * (w + kDecWaves * i).
+  // The first group's page loads are issued before Q is loaded and rotated, so
+  // the wave's first memory round trip overlaps the Q work; each later group
+  // is loaded into the same registers right after the previous one is used.
+  constexpr int kStride = kDecUnroll * kDecWaves;
+  int ent[kDecUnroll];
+  PageRegs pr[kDecUnroll];
+  const int p_first = p_begin + kDecUnroll * __builtin_amdgcn_readfirstlane(wave);
+  if (p_first < p_end) {
+    dec_fetch_group(a, b, p_first, p_begin, p_end, ent);
+#pragma unroll
+    for (int u = 0; u < kDecUnroll; ++u) {
+      if (p_first + u < p_end) dec_load_page(a, h, ent[u], p_first + u, N, lane, pr[u]);
+    }
+    dec_fetch_group(a, b, p_first + kStride, p_begin, p_end, ent);
+  }
+
   // ---- Q^T fragments: lane holds q head g, level 2lp + lane/32, half (lane/16)%2 ----
   u32x4 Qf[4];
   {
@@ -153,18 +170,7 @@ void decode_kernel(DecodeArgs a) {
   for (int db = 0; db < 8; ++db) O[db] = f32x4{};
   float m_run = NEG_INF, l_run = 0.f;
 
-  // wave w takes the groups of kDecUnroll pages that start at p_begin + kDecUnroll * (w + kDecWaves * i)
-  constexpr int kStride = kDecUnroll * kDecWaves;
-  int ent[kDecUnroll];
-  const int p_first = p_begin + kDecUnroll * __builtin_amdgcn_readfirstlane(wave);
-  if (p_first < p_end) dec_fetch_group(a, b, p_first, p_begin, p_end, ent);
   for (int p0 = p_first; p0 < p_end; p0 += kStride) {
-    PageRegs pr[kDecUnroll];
-#pragma unroll
-    for (int u = 0; u < kDecUnroll; ++u) {
-      if (p0 + u < p_end) dec_load_page(a, h, ent[u], p0 + u, N, lane, pr[u]);
-    }
-    dec_fetch_group(a, b, p0 + kStride, p_begin, p_end, ent);
 #pragma unroll
     for (int u = 0; u < kDecUnroll; ++u) {
       if (p0 + u >= p_end) break;
@@ -223,6 +229,14 @@ void decode_kernel(DecodeArgs a) {
         O[db] *= alpha;
         O[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, r.v[db]), pb, O[db], 0, 0, 0);
       }
+    }
+    const int pn = p0 + kStride;
+    if (pn < p_end) {
+#pragma unroll
+      for (int u = 0; u < kDecUnroll; ++u) {
+        if (pn + u < p_end) dec_load_page(a, h, ent[u], pn + u, N, lane, pr[u]);
+      }
+      dec_fetch_group(a, b, pn + kStride, p_begin, p_end, ent);
     }
   }
 
