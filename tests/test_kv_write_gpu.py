@@ -9,14 +9,21 @@ import helpers as H
 pytestmark = pytest.mark.gpu
 
 
-def _expected_pages(k, v, table, start, n_pages_pool, hkv, layout=0):
-    """CPU model of the cache layout for one sequence (no RoPE)."""
+def _expected_pages(k, v, table, start, n_pages_pool, hkv, layout=0, init=None):
+    """CPU model of the cache layout for one sequence (no RoPE); `init` is the
+    cache content before the write (zeros if None).  Tokens at negative
+    positions are not written."""
     P = 64
-    ek = torch.zeros((n_pages_pool, hkv, 8, 16, 16), dtype=torch.bfloat16)
-    ev = torch.zeros((n_pages_pool, hkv, 128, 16), dtype=torch.bfloat16)
+    if init is None:
+        ek = torch.zeros((n_pages_pool, hkv, 8, 16, 16), dtype=torch.bfloat16)
+        ev = torch.zeros((n_pages_pool, hkv, 128, 16), dtype=torch.bfloat16)
+    else:
+        ek, ev = init[0].clone(), init[1].clone()
     slot_of = [4 * [0, 2, 1, 3][t // 4] + t % 4 for t in range(16)]
     for t in range(k.shape[0]):
         pos = start + t
+        if pos < 0:
+            continue
         pg = table[pos // 16]
         s = pos % 16
         for lv in range(8):
@@ -68,3 +75,63 @@ def test_rope_at_write_matches_fp32_rotation(dev):
     assert (err <= torch.maximum(want.abs(), got.abs()) * 2 ** -7 + 1e-4).all(), err.max()
     # a wrong pair, sign or position would be O(1) off
     assert err.max().item() < 0.05
+
+
+def _random_cache(pool, hkv, g):
+    return (H.randn_bf16((pool, hkv, 8, 16, 16), g), H.randn_bf16((pool, hkv, 128, 16), g))
+
+
+def test_partial_pages_keep_the_other_slots(dev):
+    """A write that covers pages only in part (start 21, 45 tokens: pages 1-4)
+    into a cache full of other data changes exactly the written slots."""
+    g = torch.Generator().manual_seed(8)
+    hkv, n, start, pool = 2, 45, 21, 12
+    init = _random_cache(pool, hkv, g)
+    k = H.randn_bf16((n, hkv, H.D), g)
+    v = H.randn_bf16((n, hkv, H.D), g)
+    table = torch.randperm(pool, generator=g)[:5].to(torch.int32)
+    kc, vc = init[0].to(dev), init[1].to(dev)
+    torch.ops.atflash.kv_write(kc, vc, k[None].to(dev), v[None].to(dev),
+                               torch.tensor([start], dtype=torch.int32, device=dev), table[None].to(dev), None, 0)
+    ek, ev = _expected_pages(k, v, table.tolist(), start, pool, hkv, init=init)
+    assert torch.equal(kc.cpu(), ek)
+    assert torch.equal(vc.cpu(), ev)
+
+
+def test_token_by_token_append_equals_one_write(dev):
+    """50 single-token appends (the decode step's write) build the same pages
+    as one write of the 50 tokens."""
+    g = torch.Generator().manual_seed(9)
+    hkv, n, pool = 4, 50, 8
+    k = H.randn_bf16((n, hkv, H.D), g).to(dev)
+    v = H.randn_bf16((n, hkv, H.D), g).to(dev)
+    table = torch.randperm(pool, generator=g)[:4].to(torch.int32)[None].to(dev)
+    init = _random_cache(pool, hkv, g)
+    a = (init[0].to(dev), init[1].to(dev))
+    b = (init[0].to(dev), init[1].to(dev))
+    torch.ops.atflash.kv_write(a[0], a[1], k[None], v[None], torch.zeros(1, dtype=torch.int32, device=dev), table,
+                               None, 0)
+    for t in range(n):
+        torch.ops.atflash.kv_write(b[0], b[1], k[None, t:t + 1], v[None, t:t + 1],
+                                   torch.tensor([t], dtype=torch.int32, device=dev), table, None, 0)
+    assert torch.equal(a[0].cpu(), b[0].cpu()) and torch.equal(a[1].cpu(), b[1].cpu())
+
+
+def test_batch_with_a_negative_start(dev):
+    """Batch 2: sequence 0 starts at 5, sequence 1 at -7 (its first 7 tokens
+    have negative positions and are not written)."""
+    g = torch.Generator().manual_seed(10)
+    hkv, n, pool = 2, 40, 16
+    init = _random_cache(pool, hkv, g)
+    k = H.randn_bf16((2, n, hkv, H.D), g)
+    v = H.randn_bf16((2, n, hkv, H.D), g)
+    perm = torch.randperm(pool, generator=g).to(torch.int32)
+    tables = torch.stack([perm[:4], perm[4:8]])
+    starts = [5, -7]
+    kc, vc = init[0].to(dev), init[1].to(dev)
+    torch.ops.atflash.kv_write(kc, vc, k.to(dev), v.to(dev), torch.tensor(starts, dtype=torch.int32, device=dev),
+                               tables.to(dev).contiguous(), None, 0)
+    ek, ev = _expected_pages(k[0], v[0], tables[0].tolist(), starts[0], pool, hkv, init=init)
+    ek, ev = _expected_pages(k[1], v[1], tables[1].tolist(), starts[1], pool, hkv, init=(ek, ev))
+    assert torch.equal(kc.cpu(), ek)
+    assert torch.equal(vc.cpu(), ev)
