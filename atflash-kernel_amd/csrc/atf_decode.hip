@@ -29,6 +29,10 @@ namespace atf {
 // compiler's own wait insertion accounts for it.
 constexpr int kWaitVm = 0x0F70;
 
+// Word 3 of a raw buffer resource (no format conversion, 32-bit data format
+// field), as the raw buffer-load path of gfx9-family targets expects.
+constexpr int kBufferWord3 = 0x00020000;
+
 // max / sum over the 4 lanes {l, l^16, l^32, l^48} that hold one query head.
 __device__ __forceinline__ float quad_max(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -76,28 +80,31 @@ __device__ __forceinline__ void dec_load_page(const DecodeArgs& a, int h, int ra
   r.L = levels_of(a.lt, max(0, (N - 1) - (r.n0 + kPage - 1)));
   const int pg = __builtin_amdgcn_readfirstlane(raw);
   const bool ok = pg >= 0 && pg < a.num_pages;
-  const size_t blk = (static_cast<size_t>(ok ? pg : 0) * a.hkv + h) * kBlockElems;
-  const uint16_t* kb = a.k_cache + blk;
-  const uint16_t* vb = a.v_cache + blk;
-  const int lvl_hi = lane >> 5;
-  const int half = (lane >> 4) & 1;
-  const int tok = lane & 15;
+  // The page's K and V blocks as range-checked buffer resources: a load at or
+  // past the range returns zeros without a memory request.  K's levels are a
+  // contiguous prefix of its block, so a range of L(p) * 512 bytes reads the
+  // in-window levels and yields zeros for the others (lanes 32-63 of an odd
+  // level pair included); an invalid page entry gets an empty range.  The
+  // loads are therefore unconditional: wave-uniform base, 32-bit lane offset,
+  // immediate row offset, no per-load address arithmetic.
+  const size_t blk_bytes = (static_cast<size_t>(ok ? pg : 0) * a.hkv + h) * (kBlockElems * 2);
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.k_cache) + blk_bytes / 2, 0, ok ? r.L * (kPage * 16 * 2) : 0, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.v_cache) + blk_bytes / 2, 0, ok ? kBlockElems * 2 : 0, kBufferWord3);
+  // K: level 2lp + lane/32, token lane%16, half (lane/16)%2 of the level's 16 dims
+  const uint32_t koff = (static_cast<uint32_t>(lane >> 5) << 9) | (static_cast<uint32_t>(lane & 15) << 5) |
+                        (static_cast<uint32_t>((lane >> 4) & 1) << 4);
 #pragma unroll
-  for (int lp = 0; lp < 4; ++lp) {
-    u32x4 v = {0u, 0u, 0u, 0u};
-    const int level = 2 * lp + lvl_hi;
-    if (ok && level < r.L) v = ldg16(kb + level * 256 + tok * 16 + half * 8);
-    r.k[lp] = v;
-  }
+  for (int lp = 0; lp < 4; ++lp)
+    r.k[lp] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, koff + lp * 1024u, 0, 0));
   // V^T operand: d row 16*db + lane%16, tokens 4*(lane/16)..+3 -> stored slots.
   const int grp = lane >> 4;
   const int slot0 = 4 * ((grp == 1) ? 2 : (grp == 2 ? 1 : grp));
+  const uint32_t voff = (static_cast<uint32_t>(lane & 15) << 5) + static_cast<uint32_t>(slot0) * 2u;
 #pragma unroll
-  for (int db = 0; db < 8; ++db) {
-    u32x2 v = {0u, 0u};
-    if (ok) v = *reinterpret_cast<const u32x2*>(vb + (16 * db + tok) * 16 + slot0);
-    r.v[db] = v;
-  }
+  for (int db = 0; db < 8; ++db)
+    r.v[db] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rv, voff + db * 512u, 0, 0));
 }
 
 // two waves per SIMD: at most 256 registers per wave
