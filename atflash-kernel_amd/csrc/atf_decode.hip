@@ -182,13 +182,13 @@ void decode_kernel(DecodeArgs a) {
     for (int u = 0; u < kDecUnroll; ++u) {
       if (p0 + u >= p_end) break;
       PageRegs& r = pr[u];
+      // all four level pairs: the out-of-window levels were loaded as zeros and
+      // add exact zeros (cheaper than branching around their MFMAs)
       f32x4 S = f32x4{};
 #pragma unroll
-      for (int lp = 0; lp < 4; ++lp) {
-        if (2 * lp < r.L)
-          S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, r.k[lp]),
-                                                      __builtin_bit_cast(bf16x8, Qf[lp]), S, 0, 0, 0);
-      }
+      for (int lp = 0; lp < 4; ++lp)
+        S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, r.k[lp]),
+                                                    __builtin_bit_cast(bf16x8, Qf[lp]), S, 0, 0, 0);
       // S lane layout: q head g, tokens 4*(lane/16) + i.
       const int tok0 = r.n0 + 4 * (lane >> 4);
       const bool tail = r.n0 + kPage > N;
