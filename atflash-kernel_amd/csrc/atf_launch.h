@@ -13,9 +13,6 @@ constexpr int kPfRowsWave = 32;
 constexpr int kPfRowsWg = kPfWaves * kPfRowsWave;
 constexpr int kPfTileN = 64;
 constexpr int kPfWinN = 32;
-constexpr int kPfStageBytes = 8 * 4096;  // 4 K pages + 4 V pages
-constexpr int kPfStages = 3;             // ring: tiles t-1 (V), t (K), t+1 (loading)
-constexpr int kPfLdsBytes = kPfStages * kPfStageBytes;
 
 // Decode geometry (block_n = one page).
 constexpr int kDecMaxGroup = 16;

@@ -8,12 +8,15 @@
 //   workgroup = 8 waves = 256 consecutive query positions of one q head;
 //   wave      = 32 positions (one MFMA row block).  Waves w and w+4 share a SIMD
 //               and run one phase apart ("ping-pong"): at every step one of them
-//               issues MFMAs (PV of tile t-1, then QK of tile t) while the other
-//               runs the softmax of its current tile, so the matrix pipe and the
-//               VALU work at the same time;
-//   k-tile    = 64 keys = 4 cache pages, staged through a 3-deep LDS ring with
-//               direct global->LDS loads; the window is quantized per 32-key block
-//               ("kb"), i.e. the oracle tile is (block_m, block_n) = (32, 32).
+//               issues MFMAs (PV of the previous tile pair, then QK of the
+//               current pair) while the other runs the softmax of its current
+//               pair, so the matrix pipe and the VALU work at the same time;
+//   k-tile    = 64 keys = 4 cache pages; a phase covers a pair of tiles (128
+//               keys, 64 MFMAs with the window off), so the per-phase barrier
+//               and pipeline ramp are paid once per 128 keys.  K and V are
+//               staged through LDS rings (3 K pairs, 2 V pairs: 160 KB) with
+//               direct global->LDS loads; the window is quantized per 32-key
+//               block ("kb"), i.e. the oracle tile is (block_m, block_n) = (32, 32).
 //   S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_32x32x16_bf16: the accumulator
 //   lane l always holds query row l%32, so the online-softmax max/sum stay in the
 //   lane except one exchange with lane l^32 (v_permlane32_swap).
@@ -173,16 +176,12 @@ __device__ __forceinline__ void lds_copy_rows(const uint8_t* base, uint32_t voff
 #undef ATF_LDS_ROW
 }
 
-// Stage one 64-key tile (4 pages) into LDS: waves 0-3 copy K (first L levels)
-// of page w, waves 4-7 copy V of page w-4; `pg` is the page id (-1: missing
-// page, zero-filled).
-// `voff` is the lane's chunk offset within a copied 1 KB row (k_copy_src or
-// v_copy_src for the wave's half).
-__device__ __forceinline__ void pf_load_tile(const PrefillArgs& a, int kvh, int pg, int L, lds_u8* stage,
-                                             int wave, int lane, uint32_t voff) {
-  const int page = wave & 3;
-  const bool is_v = wave >= 4;
-  lds_u8* dst = stage + (is_v ? 4 * 4096 : 0) + page * 4096;
+// Stage one 4 KB page into LDS at `dst`: K (whole 1 KB level pairs covering
+// the first L levels) or V.  `pg` is the page id (-1: missing page,
+// zero-filled); `voff` is the lane's chunk offset within a copied 1 KB row
+// (k_copy_src or v_copy_src).
+__device__ __forceinline__ void pf_load_page(const PrefillArgs& a, int kvh, int pg, int L, bool is_v, lds_u8* dst,
+                                             int lane, uint32_t voff) {
   if (pg < 0) {
     const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
@@ -281,31 +280,44 @@ __device__ __forceinline__ void qk_tile(int L0, int L1, const lds_u8* k0, const 
   }
 }
 
+// LDS ring.  A K slot holds the K pages of one 64-key tile, a V slot its V
+// pages (4 pages of 4 KB).  Phase u reads the K of tiles 2u and 2u+1 and the V
+// of tiles 2u-2 and 2u-1, so tiles are staged in pairs: K pair u % 3 holds
+// tiles 2u, 2u+1 (three pairs: read, landing, being copied), V pair u % 2
+// holds tiles 2u, 2u+1 (two pairs: read, being copied).
+constexpr int kPfSlotBytes = 4 * 4096;
+constexpr int kPfPairBytes = 2 * kPfSlotBytes;
+constexpr int kPfKPairs = 3;
+constexpr int kPfVPairs = 2;
+constexpr int kPfVRegion = kPfKPairs * kPfPairBytes;
+constexpr int kPfLdsTotal = (kPfKPairs + kPfVPairs) * kPfPairBytes;  // 160 KB
+static_assert(kPfLdsTotal <= 160 * 1024, "gfx950 LDS");
+
 // The MFMA phase as one stream of MFMAs, each taking one 1 KB A operand from
-// LDS: stream i < 16 is PV step (ks, db) = (i/4, i%4), O[db] += V^T[db,ks] P^T[ks];
-// stream 16 + j is QK level j/2 of 32-key block j%2 (the first level starts
-// from C), 16 + 2L MFMAs in all when both blocks have L levels.  The operands
-// go through a ring of kRing registers: the read of operand i + kRing - 1 is
-// issued before MFMA i (scheduling barriers keep that order), so each read has
-// kRing - 1 MFMAs (32 cycles each) to arrive; the LDS latency under four SIMDs'
-// operand traffic is longer than one or two.  The PV part is shared by every
-// level count: it reads the first QK operands ahead in this order, which is
-// the same for any L (an operand past 2L is read and not used; its address is
-// still inside the staged tile).
+// LDS.  Stream i < 32 is PV step (page p, dim block db) = (i/4, i%4) over the
+// tile pair's 8 pages, O[db] += V^T[db, p] P^T[p]; stream 32 + j is QK level
+// j/4 of 32-key block j%4 (blocks 0, 1: first tile of the pair, 2, 3: second;
+// the first level starts from C), 32 + 4L MFMAs in all when the four blocks
+// have L levels.  The operands go through a ring of kRing registers: the read
+// of operand i + kRing - 1 is issued before MFMA i (scheduling barriers keep
+// that order), so each read has kRing - 1 MFMAs (32 cycles each) to arrive;
+// the LDS latency under four SIMDs' operand traffic is longer than one or
+// two.  The PV part is shared by every level count: it reads the first QK
+// operands ahead in this order, which is the same for any L (an operand past
+// 4L is read and not used; its address is still inside the staged pair).
 #ifndef ATF_PF_RING
 #define ATF_PF_RING 6
 #endif
 constexpr int kRing = ATF_PF_RING;
-static_assert(kRing >= 2 && kRing - 1 <= 16, "ring depth");
+static_assert(kRing - 1 >= 4 && kRing - 1 <= 32, "ring depth: the level-0 operands of all four blocks are read ahead");
 
 __device__ __forceinline__ const lds_u8* stream_src(const lds_u8* vb, const lds_u8* kb, int i) {
-  if (i < 16) return vb + (i >> 2) * 4096 + (i & 3) * 1024;
-  const int j = i - 16;
-  return kb + (j & 1) * (2 * 4096) + (j >> 1) * 512;
+  if (i < 32) return vb + (i >> 2) * 4096 + (i & 3) * 1024;
+  const int j = i - 32;
+  return kb + (j & 3) * 8192 + (j >> 2) * 512;
 }
 
 // The first kRing - 1 operands of the stream (V^T only).
-static_assert(kRing - 1 <= 16, "ring prefetch must stay within the PV operands");
 __device__ __forceinline__ void pv_prefetch(const lds_u8* vb, bf16x8 (&f)[kRing]) {
 #pragma unroll
   for (int i = 0; i < kRing - 1; ++i) {
@@ -314,10 +326,10 @@ __device__ __forceinline__ void pv_prefetch(const lds_u8* vb, bf16x8 (&f)[kRing]
   }
 }
 
-__device__ __forceinline__ void pv_stream(const lds_u8* vb, const lds_u8* kb, const bf16x8 (&Pf)[4], f32x16 (&O)[4],
+__device__ __forceinline__ void pv_stream(const lds_u8* vb, const lds_u8* kb, const bf16x8 (&Pf)[8], f32x16 (&O)[4],
                                           bf16x8 (&f)[kRing]) {
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
+  for (int i = 0; i < 32; ++i) {
     f[(i + kRing - 1) % kRing] = lds_frag(stream_src(vb, kb, i + kRing - 1));
     __builtin_amdgcn_sched_barrier(0);
     O[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[i % kRing], Pf[i >> 2], O[i & 3], 0, 0, 0);
@@ -325,27 +337,28 @@ __device__ __forceinline__ void pv_stream(const lds_u8* vb, const lds_u8* kb, co
   }
 }
 
+// QK of the four blocks with one level count L: four interleaved chains.
 template <int L>
 __device__ __forceinline__ void qk_stream(const lds_u8* kb, bf16x8 (&f)[kRing], const u32x4 (&Qf)[kLevels],
-                                          const f32x16& C, f32x16 (&S)[2]) {
-  constexpr int NS = 16 + 2 * L;
+                                          const f32x16& C, f32x16 (&S)[4]) {
+  constexpr int NS = 32 + 4 * L;
 #pragma unroll
-  for (int i = 16; i < NS; ++i) {
+  for (int i = 32; i < NS; ++i) {
     if (i + kRing - 1 < NS) f[(i + kRing - 1) % kRing] = lds_frag(stream_src(kb, kb, i + kRing - 1));
     __builtin_amdgcn_sched_barrier(0);
-    const int j = i - 16;
-    S[j & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[i % kRing], __builtin_bit_cast(bf16x8, Qf[j >> 1]),
-                                                       (j >> 1) == 0 ? C : S[j & 1], 0, 0, 0);
+    const int j = i - 32;
+    S[j & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[i % kRing], __builtin_bit_cast(bf16x8, Qf[j >> 2]),
+                                                       (j >> 2) == 0 ? C : S[j & 3], 0, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
   }
 }
 
-// P = exp2(S) of a tile packed to bf16 (the B operands of the next PV steps),
-// and the lane's partial row sum of P.
-__device__ __forceinline__ float exp_tile(const f32x16 (&S)[2], bf16x8 (&Pf)[4]) {
+// P = exp2(S) of a tile pair packed to bf16 (Pf[p] is the B operand of the PV
+// steps of page p), and the lane's partial row sum of P.
+__device__ __forceinline__ float exp_tiles(const f32x16 (&S)[4], bf16x8 (&Pf)[8]) {
   float lt = 0.f;
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
+  for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
     for (int hs = 0; hs < 2; ++hs) {
       u32x4 pk;
@@ -391,7 +404,8 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
   const int pos0 = a.q_offset + lr0;
   const int n_ktiles = (a.nk + kPfTileN - 1) / kPfTileN;
   const int last_wg = a.q_offset + min(a.nq, lr0_wg + kPfRowsWg) - 1;
-  const int t_end_wg = min(n_ktiles, last_wg / kPfTileN + 1);
+  const int T = min(n_ktiles, last_wg / kPfTileN + 1);  // tiles of the workgroup
+  const int T2 = (T + 1) & ~1;                          // rounded up to whole pairs
   const int t_end =
       (lr0 < a.nq) ? min(n_ktiles, (a.q_offset + min(a.nq, lr0 + kPfRowsWave) - 1) / kPfTileN + 1) : 0;
 
@@ -428,148 +442,190 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
   float m_ref = 0.f;      // reference max (log2 units), set by the first tile
   float l_run = 0.f;      // this lane's partial row sum relative to m_ref
   f32x16 Cm = f32x16{};   // -m_ref in every element
-  const int T = t_end_wg;
-#ifndef ATF_PF_GROUP
-#define ATF_PF_GROUP(w) ((w) >> 2)
-#define ATF_PF_RANK(w) ((w) & 3)
-#endif
-  const int grp = ATF_PF_GROUP(wave);  // ping-pong group (waves w and w+4 share a SIMD)
-  const int rank = ATF_PF_RANK(wave);  // 0..3 within the group
+  const int grp = wave >> 2;   // ping-pong group (waves w and w+4 share a SIMD)
+  const int rank = wave & 3;   // 0..3 within the group: the page of a tile this wave copies
+  const bool copies_v = grp == 1;
 
-  // Level walkers: far (keys n0..n0+31) and near (n0+32..n0+63) blocks of this
-  // wave, and the workgroup's staging count (nearest key, first row).
+  // Level walkers: the four 32-key blocks of a phase are the far (keys
+  // n0..n0+31) and near (n0+32..n0+63) halves of its two tiles; w_ld is the
+  // workgroup's staging count (nearest key, first row).
   LevelWalker w_far, w_near, w_ld;
   w_far.init(a.lt, pos0 - 31);
   w_near.init(a.lt, pos0 - 63);
   w_ld.init(a.lt, pos0_wg - 63);
 
-  // LDS ring: byte offsets of the stages holding tiles t-1, t and t+1.
-  int o_prev = 2 * kPfStageBytes, o_cur = 0, o_next = kPfStageBytes;
+  const uint32_t copy_off = static_cast<uint32_t>(copies_v ? v_copy_src(lane) : k_copy_src(lane));
+  const int k_lane = ((lane & 31) >> 4) * 4096 + (lane >> 5) * 256 + (lane & 15) * 16;
+  const int v_lane = (lane >> 5) * 512 + (lane & 31) * 16;
 
-  // ---- prologue: stage tile 0 ----
-  const int page_w = wave & 3;  // this wave's page within a tile
-  const uint32_t copy_off = static_cast<uint32_t>(wave >= 4 ? v_copy_src(lane) : k_copy_src(lane));
-  if (T > 0) pf_load_tile(a, kvh, page_id(a, fetch_page(a, b, page_w)), w_ld.advance(a.lt, 0), smem + o_cur, wave, lane, copy_off);
+  // ---- prologue ----
+  // Group 0 copies K, group 1 copies V, each wave page `rank` of a tile.  Group
+  // 0 stages the K of tiles 0 and 1 (waited for here) and requests tiles 2 and
+  // 3; group 1 zeroes V pair 1 (read with P = 0 by phase 0) and requests the V
+  // of tiles 0 and 1.  pg_a / pg_b: page-table entries of the wave's next two
+  // copies, fetched one phase ahead.
+  int pg_a, pg_b;
+  if (!copies_v) {
+    const int e0 = fetch_page(a, b, rank), e1 = fetch_page(a, b, 4 + rank);
+    const int p0 = page_id(a, e0), p1 = page_id(a, e1);
+    if (0 < T) pf_load_page(a, kvh, p0, w_ld.advance(a.lt, 0), false, smem + rank * 4096, lane, copy_off);
+    if (1 < T) pf_load_page(a, kvh, p1, w_ld.advance(a.lt, 1), false, smem + kPfSlotBytes + rank * 4096, lane, copy_off);
+  } else {
+    const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(
+            smem + kPfVRegion + kPfPairBytes + s * kPfSlotBytes + rank * 4096 + i * 1024 + lane * 16) = z;
+  }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  if (T > 0 && kPfTileN > a.nk) {  // zero V of keys past nk (0 * V must stay 0)
-    const int page = threadIdx.x >> 7;
-    const int d = threadIdx.x & 127;
-    lds_u8* vpage = smem + o_cur + 4 * 4096 + page * 4096;
-#pragma unroll
-    for (int tk = 0; tk < kPage; ++tk)
-      if (page * kPage + tk >= a.nk)
-        *reinterpret_cast<__attribute__((address_space(3))) uint16_t*>(vpage + v_lds_elem(d, v_slot(tk))) = 0;
-    __syncthreads();
+  if (!copies_v) {
+    const int e2 = fetch_page(a, b, 8 + rank), e3 = fetch_page(a, b, 12 + rank);
+    const int p2 = page_id(a, e2), p3 = page_id(a, e3);
+    if (2 < T) pf_load_page(a, kvh, p2, w_ld.advance(a.lt, 2), false, smem + kPfPairBytes + rank * 4096, lane, copy_off);
+    if (3 < T)
+      pf_load_page(a, kvh, p3, w_ld.advance(a.lt, 3), false, smem + kPfPairBytes + kPfSlotBytes + rank * 4096, lane,
+                   copy_off);
+    pg_a = fetch_page(a, b, 16 + rank);
+    pg_b = fetch_page(a, b, 20 + rank);
+  } else {
+    const int e0 = fetch_page(a, b, rank), e1 = fetch_page(a, b, 4 + rank);
+    const int p0 = page_id(a, e0), p1 = page_id(a, e1);
+    if (0 < T2) pf_load_page(a, kvh, p0, kLevels, true, smem + kPfVRegion + rank * 4096, lane, copy_off);
+    if (1 < T2) pf_load_page(a, kvh, p1, kLevels, true, smem + kPfVRegion + kPfSlotBytes + rank * 4096, lane, copy_off);
+    pg_a = fetch_page(a, b, 8 + rank);
+    pg_b = fetch_page(a, b, 12 + rank);
+    pf_barrier();  // group 1 starts one step late
   }
 
-  f32x16 S[2];
-  bf16x8 Pf[4];
+  f32x16 S[4];
+  bf16x8 Pf[8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) Pf[i] = bf16x8{};
-  // Global step k: group g runs phase k - g.  Phase 2t is the MFMA phase of
-  // tile t (PV of tile t-1, QK of tile t), phase 2t+1 its softmax.  Copies are
-  // issued in softmax phases only, so an MFMA phase never waits behind them:
-  // K of tile t+2 by group 0 in its softmax of tile t (step 2t+1), V of tile
-  // t+2 by group 1 in its softmax of tile t (step 2t+2).  Each wave waits for
-  // its copies before the barrier ending its next MFMA phase (steps 2t+2 and
-  // 2t+3); tile t+2 is first read at step 2t+4.  Tile 1 is requested before
-  // the loop.  The MFMA phase runs unconditionally (P = 0 when there is
-  // nothing to add) so the accumulators stay in place.
-  const int v_lane = 4 * 4096 + (lane >> 5) * 512 + (lane & 31) * 16;
-  // next page-table entry of this wave: tile 1 for group 0, tile 2 for group 1
-  int pg_next;
-  if (grp == 1) {
-    if (1 < T)
-      pf_load_tile(a, kvh, page_id(a, fetch_page(a, b, 4 + page_w)), w_ld.advance(a.lt, 1), smem + o_next, wave,
-                   lane, copy_off);
-    pg_next = fetch_page(a, b, 8 + page_w);
-    pf_barrier();  // group 1 starts one step late
-  } else {
-    if (1 < T)
-      pf_load_tile(a, kvh, page_id(a, fetch_page(a, b, 4 + page_w)), w_ld.advance(a.lt, 1), smem + o_next, wave,
-                   lane, copy_off);
-    pg_next = fetch_page(a, b, 8 + page_w);
-  }
-  for (int t = 0; t <= T; ++t) {
-    // ---- MFMA phase of tile t ----
+  for (int i = 0; i < 8; ++i) Pf[i] = bf16x8{};
+  // Global step k: group g runs phase k - g.  Phase 2u is the MFMA phase of
+  // tile pair u (PV of tiles 2u-2 and 2u-1, QK of tiles 2u and 2u+1), phase
+  // 2u+1 its softmax.  Copies are issued in softmax phases only, so an MFMA
+  // phase never waits behind them: K of tiles 2u+4, 2u+5 by group 0 in its
+  // softmax of pair u (step 2u+1), V of tiles 2u+2, 2u+3 by group 1 in its
+  // softmax of pair u (step 2u+2).  Each wave waits for its copies before the
+  // barrier ending its next MFMA phase (steps 2u+2 and 2u+3); both are first
+  // read at step 2u+4.  The MFMA phase runs unconditionally (P = 0 when there
+  // is nothing to add) so the accumulators stay in place.
+  const int U = T2 >> 1;
+  for (int u = 0; u <= U; ++u) {
+    // ---- MFMA phase of pair u ----
 #ifndef ATF_PF_NO_PRIO
     __builtin_amdgcn_s_setprio(1);
 #endif
     {
-      const lds_u8* kbase = smem + o_cur + ((lane & 31) >> 4) * 4096 + (lane >> 5) * 256 + (lane & 15) * 16;
-      // O^T += V^T P^T for tile t-1 (P = 0 at t = 0), then S^T = K Q^T over the
-      // surviving levels of each 32-key block of tile t (unused when the wave
-      // has no tile t).
-      const lds_u8* vb = smem + (t == 0 ? o_cur : o_prev) + v_lane;
-      const int L0 = w_far.advance(a.lt, t);
-      const int L1 = w_near.advance(a.lt, t);
+      const lds_u8* kb = smem + (u % kPfKPairs) * kPfPairBytes + k_lane;
+      const lds_u8* vb = smem + kPfVRegion + ((u + 1) & 1) * kPfPairBytes + v_lane;
+      const int L0 = w_far.advance(a.lt, 2 * u);
+      const int L1 = w_near.advance(a.lt, 2 * u);
+      const int L2 = w_far.advance(a.lt, 2 * u + 1);
+      const int L3 = w_near.advance(a.lt, 2 * u + 1);
       bf16x8 f[kRing];
       pv_prefetch(vb, f);
-      pv_stream(vb, kbase, Pf, O, f);
-      if (L0 == L1) {
+      pv_stream(vb, kb, Pf, O, f);
+      if (L0 == L3) {  // L0 <= L1 <= L2 <= L3: one level count
         switch (L0) {
-          case 8: qk_stream<8>(kbase, f, Qf, Cm, S); break;
-          case 7: qk_stream<7>(kbase, f, Qf, Cm, S); break;
-          case 6: qk_stream<6>(kbase, f, Qf, Cm, S); break;
-          case 5: qk_stream<5>(kbase, f, Qf, Cm, S); break;
-          case 4: qk_stream<4>(kbase, f, Qf, Cm, S); break;
-          case 3: qk_stream<3>(kbase, f, Qf, Cm, S); break;
-          case 2: qk_stream<2>(kbase, f, Qf, Cm, S); break;
-          default: qk_stream<1>(kbase, f, Qf, Cm, S); break;
+          case 8: qk_stream<8>(kb, f, Qf, Cm, S); break;
+          case 7: qk_stream<7>(kb, f, Qf, Cm, S); break;
+          case 6: qk_stream<6>(kb, f, Qf, Cm, S); break;
+          case 5: qk_stream<5>(kb, f, Qf, Cm, S); break;
+          case 4: qk_stream<4>(kb, f, Qf, Cm, S); break;
+          case 3: qk_stream<3>(kb, f, Qf, Cm, S); break;
+          case 2: qk_stream<2>(kb, f, Qf, Cm, S); break;
+          default: qk_stream<1>(kb, f, Qf, Cm, S); break;
         }
-      } else {  // a level boundary between the two blocks: two chains
-        qk_tile(L0, L1, kbase, kbase + 2 * 4096, Qf, f[16 % kRing], f[17 % kRing], Cm, S[0], S[1]);
+      } else {  // a level boundary inside the pair: per-tile chains
+        qk_tile(L0, L1, kb, kb + 8192, Qf, f[32 % kRing], f[33 % kRing], Cm, S[0], S[1]);
+        qk_tile(L2, L3, kb + 16384, kb + 24576, Qf, f[34 % kRing], f[35 % kRing], Cm, S[2], S[3]);
       }
     }
 #ifndef ATF_PF_NO_PRIO
     __builtin_amdgcn_s_setprio(0);
 #endif
-    // this wave's copies of tile t+1 (requested in its previous phase) land
-    // before the barrier after which tile t+1 is first read
+    // this wave's copies requested in its previous phase land before the
+    // barrier after which they are first read
     __builtin_amdgcn_s_waitcnt(kWaitVm);
+    if (copies_v && 2 * u < T2 && (2 * u + 2) * kPfTileN > a.nk) {
+      // the V of tiles 2u, 2u+1 (pair u % 2) has landed: zero the slots of keys
+      // past nk in this wave's pages (0 * V must stay 0); first read next phase
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int n0 = (2 * u + hh) * kPfTileN + rank * kPage;
+        lds_u8* vpage = smem + kPfVRegion + (u & 1) * kPfPairBytes + hh * kPfSlotBytes + rank * 4096;
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr)
+#pragma unroll
+          for (int tk = 0; tk < kPage; ++tk)
+            if (n0 + tk >= a.nk)
+              *reinterpret_cast<__attribute__((address_space(3))) uint16_t*>(vpage + v_lds_elem(lane * 2 + rr, v_slot(tk))) =
+                  0;
+      }
+    }
     pf_barrier();
     {
-      // K (group 0) or V (group 1) of tile t+2 into the stage of tile t-1:
-      // both groups have read that tile's K, and its V is read only by the
-      // MFMA phases of tile t, which end before the copy into V starts
-      const int pg = page_id(a, pg_next);
-      if (t + 2 < T) pf_load_tile(a, kvh, pg, w_ld.advance(a.lt, t + 2), smem + o_prev, wave, lane, copy_off);
-      pg_next = fetch_page(a, b, 4 * (t + 3) + page_w);
+      // K (group 0) of tiles 2u+4, 2u+5 into the pair of tiles 2u-2, 2u-1 (read
+      // by both groups in phase u-1), or V (group 1) of tiles 2u+2, 2u+3 into
+      // the pair of tiles 2u-2, 2u-1 (read by both groups' PV in phase u)
+      const int ct = 2 * u + (copies_v ? 2 : 4);
+      const int pa = page_id(a, pg_a), pb = page_id(a, pg_b);
+      lds_u8* dst = copies_v ? smem + kPfVRegion + ((u + 1) & 1) * kPfPairBytes
+                             : smem + ((u + 2) % kPfKPairs) * kPfPairBytes;
+      dst += rank * 4096;
+      const int lim = copies_v ? T2 : T;
+      if (ct < lim) pf_load_page(a, kvh, pa, copies_v ? kLevels : w_ld.advance(a.lt, ct), copies_v, dst, lane, copy_off);
+      if (ct + 1 < lim)
+        pf_load_page(a, kvh, pb, copies_v ? kLevels : w_ld.advance(a.lt, ct + 1), copies_v, dst + kPfSlotBytes, lane,
+                     copy_off);
+      pg_a = fetch_page(a, b, 4 * (ct + 2) + rank);
+      pg_b = fetch_page(a, b, 4 * (ct + 3) + rank);
     }
-    // ---- softmax phase of tile t (lane = query row) ----
-    if (t < t_end) {
-      const int n0 = t * kPfTileN;
-      const bool need_mask = (n0 + kPfTileN - 1 > pos0) || (n0 + kPfTileN > a.nk);
-      if (need_mask) {
-        // element (kb, r) holds key n0 + 4*(lane/32) + c with c = 32kb + 8(r/4) + r%4;
-        // masked when key > min(row position, nk - 1).  Selects, no branches.
-        const int thr = min(pos0 + (lane & 31), a.nk - 1) - n0 - 4 * (lane >> 5);
+    // ---- softmax phase of pair u (lane = query row) ----
+    if (2 * u < t_end) {
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+      for (int hh = 0; hh < 2; ++hh) {
+        const int tau = 2 * u + hh;
+        const int n0 = tau * kPfTileN;
+        if (tau >= t_end) {  // past this wave's last tile: P = 0
 #pragma unroll
-          for (int r = 0; r < 16; ++r)
-            S[kb][r] = (32 * kb + 8 * (r >> 2) + (r & 3) > thr) ? NEG_INF : S[kb][r];
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) S[2 * hh + kb][r] = NEG_INF;
+        } else if ((n0 + kPfTileN - 1 > pos0) || (n0 + kPfTileN > a.nk)) {
+          // element (kb, r) holds key n0 + 4*(lane/32) + c with c = 32kb + 8(r/4) + r%4;
+          // masked when key > min(row position, nk - 1).  Selects, no branches.
+          const int thr = min(pos0 + (lane & 31), a.nk - 1) - n0 - 4 * (lane >> 5);
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+              S[2 * hh + kb][r] = (32 * kb + 8 * (r >> 2) + (r & 3) > thr) ? NEG_INF : S[2 * hh + kb][r];
+        }
       }
       // S holds score - m_ref, so every P = exp2(S) is at most 256 unless a
       // score exceeds m_ref by more than 8; P >= 0, so that shows as a partial
       // row sum above 256 (or an infinite one).  Only then, and on the first
-      // tile (key 0 is visible to every row, so its max is finite), is the row
+      // pair (key 0 is visible to every row, so its max is finite), is the row
       // max taken: where it exceeds m_ref by more than 8 (always on the first
-      // tile), m_ref moves up to it, O and l are rescaled, and the tile's P is
+      // pair), m_ref moves up to it, O and l are rescaled, and the pair's P is
       // computed again from the shifted scores (shift 0 for the other lanes).
-      float lt = exp_tile(S, Pf);
-      if (__builtin_amdgcn_ballot_w64((t == 0) || !(lt <= 256.f)) != 0) {
+      float lt = exp_tiles(S, Pf);
+      if (__builtin_amdgcn_ballot_w64((u == 0) || !(lt <= 256.f)) != 0) {
         float mx = NEG_INF;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
           for (int r = 0; r < 16; ++r) mx = fmaxf(mx, S[kb][r]);
         mx = pair_max(mx);
-        const bool grow = (t == 0) || mx > kLazyRescaleLog2;
+        const bool grow = (u == 0) || mx > kLazyRescaleLog2;
         if (__builtin_amdgcn_ballot_w64(grow) != 0) {
           const float delta = grow ? mx : 0.f;
-          if (t > 0) {
+          if (u > 0) {
             const float alpha = fast_exp2(-delta);
             l_run *= alpha;
 #pragma unroll
@@ -579,39 +635,20 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
 #pragma unroll
           for (int i = 0; i < 16; ++i) Cm[i] = -m_ref;
 #pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
+          for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) S[kb][r] -= delta;
-          lt = exp_tile(S, Pf);
+          lt = exp_tiles(S, Pf);
         }
       }
       l_run += lt;
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) Pf[i] = bf16x8{};
+      for (int i = 0; i < 8; ++i) Pf[i] = bf16x8{};
     }
     pf_barrier();
-    // Tile t+1 has landed; group 0 zeroes the V of keys past nk in a partial
-    // last tile (read no earlier than two barriers later).
-    if (grp == 0 && t + 1 < T && (t + 1) * kPfTileN + kPfTileN > a.nk) {
-      const int n0 = (t + 1) * kPfTileN;
-      lds_u8* vpage = smem + o_next + 4 * 4096 + rank * 4096;
-#pragma unroll
-      for (int rr = 0; rr < 2; ++rr) {
-#pragma unroll
-        for (int tk = 0; tk < kPage; ++tk)
-          if (n0 + rank * kPage + tk >= a.nk)
-            *reinterpret_cast<__attribute__((address_space(3))) uint16_t*>(vpage + v_lds_elem(lane * 2 + rr, v_slot(tk))) =
-                0;
-      }
-    }
-    // rotate the ring: tile t+1 becomes current
-    const int o_old = o_prev;
-    o_prev = o_cur;
-    o_cur = o_next;
-    o_next = o_old;
   }
-  if (grp == 0) __syncthreads();  // group 0 ends one step late
+  if (!copies_v) __syncthreads();  // group 0 ends one step late
 
   // ---- epilogue: normalise and store ----
   const float l = pair_sum(l_run);
@@ -656,12 +693,12 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t s) {
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kPfLdsBytes);
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kPfLdsTotal);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
   const int blocks = a.batch * a.n_qgroups * a.hq * 8;
-  hipLaunchKernelGGL(prefill_kernel, dim3(blocks), dim3(kPfWaves * 64), kPfLdsBytes, s, a);
+  hipLaunchKernelGGL(prefill_kernel, dim3(blocks), dim3(kPfWaves * 64), kPfLdsTotal, s, a);
   return hipGetLastError();
 }
 
