@@ -39,6 +39,10 @@ CASES = [
     ("ragged_77", 1, 77, 8, 2, 1e4, 2.0, True),
     ("ragged_1000_b2", 2, 1000, 8, 2, 1e4, 0.5, True),
     ("tiny_1", 1, 1, 4, 4, 1e4, 2.0, True),
+    # odd 64-key tile counts (the last tile pair half empty) and partial last pages
+    ("odd_tiles_150", 1, 150, 8, 2, 1e4, 2.0, True),
+    ("odd_tiles_700_off", 1, 700, 8, 2, 1e4, None, True),
+    ("odd_tiles_320_b2", 2, 320, 28, 4, 1e7, 64.0, True),
 ]
 
 
@@ -88,10 +92,13 @@ def test_window_off_equals_k_inf_bitwise(dev):
     assert torch.equal(a.cpu(), b.cpu())
 
 
-@pytest.mark.parametrize("k_ret", [2.0, None])
-def test_chunked_equals_single_shot_bitwise(k_ret, dev):
+@pytest.mark.parametrize("k_ret,chunk", [(2.0, 512), (None, 512), (2.0, 192)])
+def test_chunked_equals_single_shot_bitwise(k_ret, chunk, dev):
     """Gate C0 at kernel level: prefill in chunks (q_offset multiple of 64)
-    against the growing paged cache equals the single-shot prefill bit for bit."""
+    against the growing paged cache equals the single-shot prefill bit for bit.
+    Chunks of 192 keys leave an odd number of 64-key tiles in every other
+    chunk."""
+    print(f"[prefill chunked] k={k_ret} chunk={chunk}", flush=True)
     from atflash import atflash_window as AW, interface, rope as R
     from atflash.cache import PagedKVCache
     base, N, hq, hkv = 1e7, 1536, 28, 4
@@ -107,8 +114,8 @@ def test_chunked_equals_single_shot_bitwise(k_ret, dev):
     cache.pages[0] = perm
     table = cache.page_table([0])
     outs = []
-    for c0 in range(0, N, 512):
-        c1 = c0 + 512
+    for c0 in range(0, N, chunk):
+        c1 = c0 + chunk
         starts = torch.tensor([c0], dtype=torch.int32, device=dev)
         torch.ops.atflash.kv_write(cache.k, cache.v, k[:, c0:c1], v[:, c0:c1], starts, table, rt, 0)
         o, _ = interface.prefill_paged(q[:, c0:c1], cache, table, nk=c1, q_offset=c0, zhi=zhi, rope=rt)
