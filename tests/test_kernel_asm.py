@@ -239,9 +239,27 @@ def test_prefill_kernel_does_not_spill(kernel_asm):
     assert spill and int(spill.group(1)) == 0
 
 
+def pipelined_runs(waits, depth=3):
+    """Lengths of the maximal runs counted by longest_pipelined_run."""
+    runs, run = [], 0
+    for w in waits:
+        if w is None or w >= depth:
+            run += 1
+        else:
+            if run:
+                runs.append(run)
+            run = 0
+    if run:
+        runs.append(run)
+    return runs
+
+
 def test_prefill_operand_ring_keeps_lds_reads_in_flight(kernel_asm):
-    # the PV stream (16 MFMAs) and the 8-level QK stream each run with the
-    # operand reads of several later MFMAs still outstanding
+    # the PV stream of a tile pair (32 MFMAs) and the 8-level QK stream of its
+    # four 32-key blocks (32 MFMAs, the ring draining over the last three) run
+    # with the operand reads of several later MFMAs still outstanding
     waits = lds_waits_before_mfma(kernel_asm["atf_prefill.hip"], "_ZN3atf14prefill_kernelENS_11PrefillArgsE")
-    assert len(waits) >= 32
-    assert longest_pipelined_run(waits) >= 15, waits
+    assert len(waits) >= 64
+    runs = sorted(pipelined_runs(waits), reverse=True)
+    assert runs[0] >= 31, runs
+    assert len(runs) >= 2 and runs[1] >= 25, runs
