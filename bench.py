@@ -10,7 +10,10 @@ bf16 N(0,1) synthetic tensors from a fixed seed.
            load), for window OFF, k = 2 and k = 64;
   decode   one decode step (batch 1, query at position N-1) over a paged cache of
            N tokens whose pages are randomly permuted; four cache copies (> 1 GiB)
-           are rotated so the 256 MB MALL cannot hold the working set.
+           are rotated so the 256 MB MALL cannot hold the working set;
+  kv_write the paged-cache writer over the same N tokens (K rotated and
+           level-blocked, V transposed into pages), timed as one batch of 4*K
+           back-to-back launches (`roofline_kv_write`, HBM bound).
 A step is one such call.  W untimed warm-up steps, then exactly K timed steps per
 configuration (decode: 40*K), each bracketed by HIP events on the launch
 stream, with device synchronisation around the timed region.  Decode is also
@@ -22,7 +25,9 @@ configuration's numbers are in `detail`.
 roofline  prefill attention kernel (MFMA bound): algorithmic FLOPs per launch
           (2*Hq*N^2*d window OFF; Hq*N^2*d*(1+s) window ON, s = QK slice ratio
           at the kernel's (32, 32) tiles) / mean kernel time, against 2.5 PFLOP/s;
-          the decode kernel (HBM bound) is in `roofline_decode`.
+          the decode kernel (HBM bound) is in `roofline_decode`, the cache
+          writer in `roofline_kv_write` (K and V read and written once plus one
+          RoPE table row per position).
 cpu_baseline  the oracle's fp32 banded reference (oracle/attention.py) on the
           host cores, on a sample of 32-row query tiles of the same 128K prefill,
           extrapolated to the whole prefill (cost is linear in the tile position).
@@ -136,6 +141,15 @@ def bench_gpu(args):
                                    rt, 0)
         caches.append(cache)
         tables.append(tab)
+    # ---- KV-cache writer: the whole sequence (RoPE'd K, transposed V) into the
+    # first pool again, timed as one batch of back-to-back launches ----
+    if args.only in ("all", "kv_write"):
+        z0 = torch.zeros(1, dtype=torch.int32, device=dev)
+        fw = lambda: torch.ops.atflash.kv_write(caches[0].k, caches[0].v, k, v, z0, tables[0], rt, 0)  # noqa: E731
+        for _ in range(args.warmup):
+            fw()
+        res["kv_write"] = {"batch_mean_ms": _events_time_batch(fw, args.steps * 4)}
+        print(f"[bench] kv_write: {res['kv_write']['batch_mean_ms'] * 1e3:.1f} us", flush=True)
     qd = torch.randn((1, HQ, D), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
     seq = torch.tensor([N], dtype=torch.int32, device=dev)
     del q, k, v
@@ -207,7 +221,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--n", type=int, default=131072)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=("all", "prefill", "decode", "copy"), default="all",
+    ap.add_argument("--only", choices=("all", "prefill", "decode", "kv_write", "copy"), default="all",
                     help="run one workload (for profiler runs); 'copy' is a plain 1 GiB device copy "
                          "used to calibrate the FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
@@ -257,6 +271,13 @@ def main():
         dec[name] = {"bytes": nbytes, "GBps": nbytes / t / 1e9, "frac": nbytes / t / PEAK_HBM,
                      "us_per_launch": t * 1e6}
 
+    # KV-cache writer: K and V read once and written once, plus the RoPE table
+    # row (64 (cos, sin) fp32 pairs) of each position once
+    kvw_bytes = N * HKV * D * 2 * 4 + N * (D // 2) * 2 * 4
+    kvw_t = res["kv_write"]["batch_mean_ms"] * 1e-3
+    kvw = {"bytes": kvw_bytes, "GBps": kvw_bytes / kvw_t / 1e9, "frac": kvw_bytes / kvw_t / PEAK_HBM,
+           "us_per_launch": kvw_t * 1e6}
+
     tr = _traffic()
 
     def traffic_of(kernel, window):
@@ -268,6 +289,7 @@ def main():
         roof[name]["traffic"] = traffic_of("prefill_kernel", name)
     for name in dec:
         dec[name]["traffic"] = traffic_of("decode_kernel", name)
+    kvw["traffic"] = traffic_of("kv_write_kernel", "all")
 
     pre = res["prefill"]
     line = {
@@ -294,6 +316,10 @@ def main():
         "roofline_decode": {"bound": "hbm", "achieved": dec["off"]["GBps"], "peak": PEAK_HBM / 1e9,
                             "unit": "GB/s", "frac": dec["off"]["frac"], "traffic": dec["off"]["traffic"],
                             "kernel": "atf::decode_kernel, window OFF", "per_window": dec},
+        "roofline_kv_write": {"bound": "hbm", "achieved": kvw["GBps"], "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                              "frac": kvw["frac"], "traffic": kvw["traffic"], "bytes": kvw_bytes,
+                              "kernel": f"atf::kv_write_kernel, {N} tokens x {HKV} kv heads",
+                              "us_per_launch": kvw["us_per_launch"]},
         "detail": {
             "prefill_ms": {n: pre[n]["median_ms"] for n in pre},
             "prefill_attn_kernel_ms": {n: attn[n]["median_ms"] for n in attn},
@@ -305,6 +331,7 @@ def main():
             "slice_ratios": sr,
             "ceilings": {n: {"prefill": 2 / (1 + sr[n]["s_prefill"]), "decode": 2 / (1 + sr[n]["s_decode"])}
                          for n in sr},
+            "kv_write_us": kvw["us_per_launch"],
             "decode_pool_bytes": res["decode_pool_bytes"],
             "timed_region_wall_s": wall,
             "stats": res,
