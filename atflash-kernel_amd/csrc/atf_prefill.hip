@@ -305,10 +305,7 @@ static_assert(kPfLdsTotal <= 160 * 1024, "gfx950 LDS");
 // two.  The PV part is shared by every level count: it reads the first QK
 // operands ahead in this order, which is the same for any L (an operand past
 // 4L is read and not used; its address is still inside the staged pair).
-#ifndef ATF_PF_RING
-#define ATF_PF_RING 6
-#endif
-constexpr int kRing = ATF_PF_RING;
+constexpr int kRing = 6;  // 5 measures the same, 7 about 1% slower
 static_assert(kRing - 1 >= 4 && kRing - 1 <= 32, "ring depth: the level-0 operands of all four blocks are read ahead");
 
 __device__ __forceinline__ const lds_u8* stream_src(const lds_u8* vb, const lds_u8* kb, int i) {
@@ -516,9 +513,7 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
   const int U = T2 >> 1;
   for (int u = 0; u <= U; ++u) {
     // ---- MFMA phase of pair u ----
-#ifndef ATF_PF_NO_PRIO
     __builtin_amdgcn_s_setprio(1);
-#endif
     {
       const lds_u8* kb = smem + (u % kPfKPairs) * kPfPairBytes + k_lane;
       const lds_u8* vb = smem + kPfVRegion + ((u + 1) & 1) * kPfPairBytes + v_lane;
@@ -545,9 +540,7 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
         qk_tile(L2, L3, kb + 16384, kb + 24576, Qf, f[34 % kRing], f[35 % kRing], Cm, S[2], S[3]);
       }
     }
-#ifndef ATF_PF_NO_PRIO
     __builtin_amdgcn_s_setprio(0);
-#endif
     // this wave's copies requested in its previous phase land before the
     // barrier after which they are first read
     __builtin_amdgcn_s_waitcnt(kWaitVm);
