@@ -57,6 +57,23 @@ def test_prefill_matches_oracle(name, B, N, hq, hkv, base, k_ret, rope, dev):
     print(f"  max {mx:.3e} mean {mean:.3e}")
 
 
+@pytest.mark.parametrize("q_offset,nq,k_ret", [(100, 150, 2.0), (37, 300, None), (1000, 77, 64.0)])
+def test_prefill_query_offset_matches_oracle(q_offset, nq, k_ret, dev):
+    """A query chunk at an offset that is not a multiple of 32 (bottom-right
+    causal, Nq < Nk): the 32-row tiles start at q_offset in the kernel and in
+    the oracle alike."""
+    print(f"[prefill offset] q_offset={q_offset} nq={nq} k={k_ret}", flush=True)
+    base, hq, hkv = 1e4, 8, 2
+    nk = q_offset + nq
+    q, k, v = H.qkv(1, nk, hq, hkv, seed=q_offset)
+    qc = q[:, q_offset:].contiguous()
+    out, lse = _run(qc, k, v, base, k_ret, True, dev)
+    ref = H.prefill_oracle(qc, k, v, base, float("inf") if k_ret is None else k_ret, True, q_offset=q_offset)
+    mx, mean = H.assert_close(out, ref, f"offset {q_offset}")
+    assert torch.isfinite(lse).all()
+    print(f"  max {mx:.3e} mean {mean:.3e}")
+
+
 def test_prefill_reference_tolerance_rule(dev):
     """The reference's acceptance rule: max err <= 2 * max|ref16 - ref32| + 2e-3."""
     q, k, v = H.qkv(1, 1024, 24, 8, seed=777)
