@@ -204,6 +204,27 @@ __device__ __forceinline__ void pf_load_page(const PrefillArgs& a, int kvh, int 
   }
 }
 
+// pf_load_page for the tile loop: the page's source is cbase + pg * pstride,
+// with the cache base (offset to the kv head) and the page stride computed once
+// before the loop, so the copy does not reload kernel arguments.
+__device__ __forceinline__ void stage_page(const uint8_t* cbase, uint32_t pstride, int pg, int rows, lds_u8* dst,
+                                           int lane, uint32_t voff) {
+  if (pg < 0) {
+    const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(dst + i * 1024 + lane * 16) = z;
+    return;
+  }
+  const uint8_t* src = cbase + static_cast<size_t>(static_cast<uint32_t>(pg)) * pstride;
+  switch (rows) {
+    case 4: lds_copy_rows<4>(src, voff, dst); break;
+    case 3: lds_copy_rows<3>(src, voff, dst); break;
+    case 2: lds_copy_rows<2>(src, voff, dst); break;
+    default: lds_copy_rows<1>(src, voff, dst); break;
+  }
+}
+
 // S^T (32 keys x 32 rows) of one 32-key block over its first L levels: one MFMA
 // chain, the operand of level l+1 read from LDS while level l's MFMA runs.  `a`
 // holds the level-0 operand on entry.
@@ -510,6 +531,11 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
   // barrier ending its next MFMA phase (steps 2u+2 and 2u+3); both are first
   // read at step 2u+4.  The MFMA phase runs unconditionally (P = 0 when there
   // is nothing to add) so the accumulators stay in place.
+  // the copying group's cache at this kv head and the page stride, computed
+  // once (loop invariants)
+  const uint8_t* cbase =
+      reinterpret_cast<const uint8_t*>(copies_v ? a.v_cache : a.k_cache) + static_cast<size_t>(kvh) * 4096;
+  const uint32_t pstride = static_cast<uint32_t>(a.hkv) * 4096u;
   const int U = T2 >> 1;
   for (int u = 0; u <= U; ++u) {
     // ---- MFMA phase of pair u ----
@@ -571,10 +597,11 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
                              : smem + ((u + 2) % kPfKPairs) * kPfPairBytes;
       dst += rank * 4096;
       const int lim = copies_v ? T2 : T;
-      if (ct < lim) pf_load_page(a, kvh, pa, copies_v ? kLevels : w_ld.advance(a.lt, ct), copies_v, dst, lane, copy_off);
+      // whole 1 KB level pairs for K (an odd L also copies level L, which is not read)
+      if (ct < lim) stage_page(cbase, pstride, pa, copies_v ? 4 : (w_ld.advance(a.lt, ct) + 1) >> 1, dst, lane, copy_off);
       if (ct + 1 < lim)
-        pf_load_page(a, kvh, pb, copies_v ? kLevels : w_ld.advance(a.lt, ct + 1), copies_v, dst + kPfSlotBytes, lane,
-                     copy_off);
+        stage_page(cbase, pstride, pb, copies_v ? 4 : (w_ld.advance(a.lt, ct + 1) + 1) >> 1, dst + kPfSlotBytes, lane,
+                   copy_off);
       pg_a = fetch_page(a, b, 4 * (ct + 2) + rank);
       pg_b = fetch_page(a, b, 4 * (ct + 3) + rank);
     }
