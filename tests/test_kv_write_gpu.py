@@ -35,10 +35,13 @@ def _expected_pages(k, v, table, start, n_pages_pool, hkv, layout=0, init=None):
     return ek, ev
 
 
-@pytest.mark.parametrize("layout", [0, 1])
-def test_cache_layout_bit_exact(layout, dev):
+@pytest.mark.parametrize("layout,hkv", [(0, 4), (1, 4), (0, 6), (1, 8)])
+def test_cache_layout_bit_exact(layout, hkv, dev):
+    """The writer covers a page's kv heads four at a time: 6 heads leave the
+    second pass half empty, 8 fill two passes."""
+    print(f"[kv_write layout] layout={layout} hkv={hkv}", flush=True)
     g = torch.Generator().manual_seed(4)
-    hkv, n, start, pool = 4, 203, 37, 40
+    n, start, pool = 203, 37, 40
     k = H.randn_bf16((n, hkv, H.D), g)
     v = H.randn_bf16((n, hkv, H.D), g)
     table = torch.randperm(pool, generator=g)[:-(-(start + n) // 16)].to(torch.int32)
