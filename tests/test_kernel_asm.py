@@ -220,6 +220,42 @@ def kernel_asm(tmp_path_factory):
     return out
 
 
+def test_kernel_sources_assemble(tmp_path):
+    """The `-S` listing above is never run through the assembler, so an inline
+    assembly operand the assembler rejects (a vector register where the
+    instruction needs a scalar one) only shows when an object is built: every
+    kernel source is assembled to a device object here."""
+    B = _hipcc_or_skip()
+    flags = [f for f in B.COMMON if not f.startswith("-Rpass")]
+    for src in B.sources():
+        if not src.endswith(".hip"):
+            continue
+        dst = os.path.join(tmp_path, os.path.basename(src) + ".o")
+        p = subprocess.run([B.HIPCC, *flags, "-I", B.CSRC, "--cuda-device-only", "-c", src, "-o", dst],
+                           capture_output=True, text=True)
+        assert p.returncode == 0, p.stderr[-3000:]
+
+
+def test_assembling_catches_a_planted_vector_operand(tmp_path):
+    """Planted: a divergent value under an "s" constraint.  The `-S` listing
+    accepts it; assembling rejects it."""
+    B = _hipcc_or_skip()
+    src = tmp_path / "planted.hip"
+    src.write_text('#include <hip/hip_runtime.h>\n'
+                   '__global__ void k(int* o) {\n'
+                   '  int x = threadIdx.x * 3;\n'
+                   '  asm volatile("s_cmp_le_i32 %0, 1" :: "s"(x) : "scc");\n'
+                   '  o[threadIdx.x] = x;\n'
+                   '}\n')
+    flags = [f for f in B.COMMON if not f.startswith("-Rpass")]
+    listing = subprocess.run([B.HIPCC, *flags, "--cuda-device-only", "-S", str(src), "-o", str(tmp_path / "p.s")],
+                             capture_output=True, text=True)
+    obj = subprocess.run([B.HIPCC, *flags, "--cuda-device-only", "-c", str(src), "-o", str(tmp_path / "p.o")],
+                         capture_output=True, text=True)
+    assert listing.returncode == 0, listing.stderr[-2000:]
+    assert obj.returncode != 0 and "invalid operand" in obj.stderr
+
+
 def test_no_lds_read_hazards(kernel_asm):
     for name, asm in kernel_asm.items():
         assert lds_read_hazards(asm) == [], name
