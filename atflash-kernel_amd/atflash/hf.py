@@ -1,75 +1,312 @@
-"""HuggingFace attention-interface hook.
+"""HuggingFace integration: the attention-interface hook and a paged KV cache.
 
 Mirrors the reference's hook (e2e_pipeline/atflash_e2e_fafi.py:81-131): an
 attention function registered with transformers' AttentionInterface under a
 name without "flash" in it (transformers v5 routes such names to its own
 FlashAttention path, e2e:127-130), dispatching on the query length:
 
-* L == 1  -> windowed split-KV decode against the whole K/V the model passes;
+* L == 1  -> windowed split-KV decode;
 * L > 1   -> windowed causal prefill, bottom-right aligned when L < S
              (a continued/chunked prefill).
 
-HF applies RoPE before the attention call, so q and k arrive rotated in the
-half-split (rotate_half) layout; the kernels take that layout as is (the
-reference's head-dim permutation patch, e2e:183-192, is not needed).  The
+RoPE.  The reference patches the model's RoPE so that q and k come out in its
+wavelength-sorted layout (e2e:183-192).  Here the kernels read the half-split
+(rotate_half) layout directly, and by default they also apply RoPE themselves
+(`rope_at_load=True`): register() swaps the model's rotary-embedding module for
+one that returns cos = 1 and sin = 0, which makes HF's apply_rotary_pos_emb the
+identity bit for bit, and the kernels rotate K when it is written to the cache
+and Q when it is loaded, in fp32 with the model's real inverse frequencies (and
+its attention scaling).  Q is then rounded to bf16 once, after rotation and the
+softmax scale; with HF's rotation the scaled, already-rounded bf16 Q would be
+rounded a second time, which doubles the score error for peaky attention.
+rope_at_load=False keeps HF's RoPE and passes pre-rotated q and k.  The
 attention mask is not used: like the reference's hook, this assumes causal
 attention over unpadded sequences.  window=off routes the same kernels with no
 window table (plain causal attention).
-"""
-import torch
 
+Where the K/V live.  The reference's decode reads the HF cache in place (HND
+view of the DynamicCache tensors, e2e:100-110).  The kernels here read a paged,
+level-blocked cache instead, so the serving path is `PagedCache`: an HF `Cache`
+whose per-layer `update` appends the new keys and values to that layer's pages
+with the cache-writer kernel (rotating K there with rope_at_load) and returns
+the chunk itself.  The hook recognises a layer of a bound PagedCache by
+the identity of the key tensor it receives and runs prefill / decode directly
+on the pages: no call re-packs the history.  With any other cache (HF's
+DynamicCache passes the whole history as key/value) the hook packs that history
+into a temporary paged cache per call -- correct, but it rewrites the whole
+context every call, so long contexts should use PagedCache.
+"""
+import weakref
+
+import torch
+from torch import nn
+
+try:  # transformers is only needed for the cache class and registration
+    from transformers.cache_utils import Cache, CacheLayerMixin
+except ImportError:  # pragma: no cover - the package works without transformers
+    Cache = object
+    CacheLayerMixin = object
+
+from . import _lib
 from . import interface as I
 from . import ops
 from .model_tables import ModelWindow, window_from_config
 
 ATTN_NAME = "atf_window"
+PAGE = _lib.PAGE_SIZE
+
+
+class PagedLayer(CacheLayerMixin):
+    """One model layer's K/V pages (the kernels' layout, see atflash.cache)."""
+
+    is_compileable = False
+    is_sliding = False
+    supports_early_init = False
+
+    def __init__(self, owner: "PagedCache", layer_idx: int):
+        super().__init__()
+        n_pages = owner.batch * owner.pages_per_seq
+        self.owner = owner
+        self.layer_idx = layer_idx
+        self.k = torch.zeros((n_pages, owner.num_kv_heads, _lib.LEVELS, PAGE, 16), dtype=torch.bfloat16,
+                             device=owner.device)
+        self.v = torch.zeros((n_pages, owner.num_kv_heads, _lib.HEAD_DIM, PAGE), dtype=torch.bfloat16,
+                             device=owner.device)
+        self.length = 0       # tokens written (every sequence of the batch has the same length)
+        self.prev_length = 0  # length before the last update (the last chunk's first position)
+        self.last_key = None  # the key tensor of the last update (the hook's identity check)
+        self.is_initialized = True
+
+    def lazy_initialization(self, key_states, value_states):
+        return None
+
+    def update(self, key_states, value_states, *args, **kwargs):
+        """Append key/value [B, Hkv, L, 128] at positions length .. length+L-1
+        (K rotated at write when the cache has a RoPE table) and return them
+        unchanged."""
+        o = self.owner
+        B, hkv, L, d = key_states.shape
+        if B != o.batch or hkv != o.num_kv_heads or d != _lib.HEAD_DIM:
+            raise ValueError(f"key states {tuple(key_states.shape)} do not fit this cache "
+                             f"(batch {o.batch}, kv heads {o.num_kv_heads}, head dim {_lib.HEAD_DIM})")
+        if self.length + L > o.capacity:
+            raise ValueError(f"PagedCache holds {o.capacity} tokens per sequence; "
+                             f"{self.length} + {L} would not fit")
+        ops.kv_write(self.k, self.v, key_states.transpose(1, 2), value_states.transpose(1, 2),
+                     o.start_positions(self.length), o.page_table, o.rope_cs, _lib.LAYOUT_HALF_SPLIT)
+        self.prev_length = self.length
+        self.length += L
+        self.last_key = key_states
+        return key_states, value_states
+
+    def get_mask_sizes(self, query_length: int):
+        return self.length + query_length, 0
+
+    def get_seq_length(self) -> int:
+        return self.length
+
+    def get_max_length(self) -> int:
+        return self.owner.capacity
+
+    def reset(self) -> None:
+        # pages past `length` are never read, so they need not be cleared
+        self.length = self.prev_length = 0
+        self.last_key = None
+
+    def crop(self, tokens_to_remove: int) -> None:
+        n = abs(int(tokens_to_remove)) if tokens_to_remove <= 0 else self.length - int(tokens_to_remove)
+        self.length = max(0, self.length - max(0, n))
+        self.prev_length = min(self.prev_length, self.length)
+        self.last_key = None
+
+    def reorder_cache(self, beam_idx):
+        raise NotImplementedError("PagedCache does not support beam search")
+
+    def batch_repeat_interleave(self, repeats: int):
+        raise NotImplementedError("PagedCache does not support batch expansion")
+
+    def batch_select_indices(self, indices):
+        raise NotImplementedError("PagedCache does not support batch selection")
+
+
+class PagedCache(Cache):
+    """HF Cache over per-layer paged K/V in the kernels' layout.
+
+    One page table serves every layer (all layers of a sequence grow together);
+    sequence b owns pages [b * pages_per_seq, (b + 1) * pages_per_seq).  Memory
+    is allocated up front: batch * ceil(capacity / 16) pages per layer, 8 KB per
+    page and kv head (a 1M-token Qwen2.5-7B layer with 4 kv heads: 2 GB).
+    """
+
+    def __init__(self, config, batch: int, capacity: int, device="cuda", rope_cs=None):
+        """rope_cs: fp32 [>= capacity, 64, 2] (cos, sin) table when the keys
+        arrive unrotated (RoPE applied at write), None when they arrive rotated."""
+        from .model_tables import head_dim_of
+        if head_dim_of(config) != _lib.HEAD_DIM:
+            raise ValueError(f"head_dim {head_dim_of(config)} unsupported (this build supports {_lib.HEAD_DIM})")
+        if rope_cs is not None and rope_cs.shape[0] < capacity:
+            raise ValueError(f"rope table has {rope_cs.shape[0]} positions, the cache holds {capacity}")
+        self.rope_cs = rope_cs
+        self.batch = int(batch)
+        self.capacity = int(capacity)
+        self.num_kv_heads = int(getattr(config, "num_key_value_heads", None) or config.num_attention_heads)
+        self.device = torch.device(device)
+        self.pages_per_seq = -(-self.capacity // PAGE)
+        self.page_table = torch.arange(self.batch * self.pages_per_seq, dtype=torch.int32,
+                                       device=self.device).view(self.batch, self.pages_per_seq)
+        self._pos = (None, None)   # (value, device int32 [batch] tensor), reused by every layer of a step
+        self._lens = (None, None)
+        layers = []
+        super().__init__(layers=layers)
+        for i in range(int(config.num_hidden_layers)):
+            layers.append(PagedLayer(self, i))
+
+    def start_positions(self, start: int) -> torch.Tensor:
+        if self._pos[0] != start:
+            self._pos = (start, torch.full((self.batch,), start, dtype=torch.int32, device=self.device))
+        return self._pos[1]
+
+    def seq_lens(self, n: int) -> torch.Tensor:
+        if self._lens[0] != n:
+            self._lens = (n, torch.full((self.batch,), n, dtype=torch.int32, device=self.device))
+        return self._lens[1]
+
+    def layer_of(self, layer_idx, key):
+        """The layer whose last update returned `key`, or None."""
+        if layer_idx is None or layer_idx >= len(self.layers):
+            return None
+        lyr = self.layers[layer_idx]
+        return lyr if lyr.last_key is key else None
+
+
+class IdentityRotary(nn.Module):
+    """Stands in for a model's rotary-embedding module when the kernels apply
+    RoPE: cos = 1 and sin = 0 make apply_rotary_pos_emb return q and k
+    unchanged (q * 1 + rotate_half(q) * 0 == q in any dtype)."""
+
+    def __init__(self, original: nn.Module):
+        super().__init__()
+        self.original = original
+
+    def forward(self, x, position_ids):
+        # [batch, seq, 1]: broadcasts over the head dim in apply_rotary_pos_emb
+        shape = (position_ids.shape[0], position_ids.shape[-1], 1)
+        one = torch.ones((1, 1, 1), dtype=x.dtype, device=x.device)
+        return one.expand(shape), torch.zeros_like(one).expand(shape)
 
 
 class WindowAttention:
-    """The registered attention function; `mode` is "win" (window on) or "off"."""
+    """The registered attention function; `mode` is "win" (window on) or "off".
+    With rope_at_load, q and k reach it unrotated (see IdentityRotary)."""
 
-    def __init__(self, window: ModelWindow, mode: str = "win"):
+    def __init__(self, window: ModelWindow, mode: str = "win", rope_at_load: bool = True):
         if mode not in ("win", "off"):
             raise ValueError("mode must be 'win' or 'off'")
         self.window = window
         self.mode = mode
+        self.rope_at_load = bool(rope_at_load)
+        self._caches = weakref.WeakSet()
+        self._rope = {}  # device -> fp32 (cos, sin) table, grown on demand
+
+    def rope_table(self, n: int, device):
+        """The (cos, sin) table for positions 0..n-1 (None without rope_at_load)."""
+        if not self.rope_at_load:
+            return None
+        dev = torch.device(device)
+        t = self._rope.get(dev)
+        if t is None or t.shape[0] < n:
+            t = self.window.rope_table(max(int(n), 16), dev)
+            self._rope[dev] = t
+        return t
+
+    def new_cache(self, config, batch: int, capacity: int, device="cuda") -> PagedCache:
+        """A PagedCache bound to this hook (pass it as past_key_values)."""
+        if capacity - 1 > self.window.n_ctx:
+            raise ValueError(f"capacity {capacity} exceeds the window tables' n_ctx {self.window.n_ctx}")
+        cache = PagedCache(config, batch, capacity, device, rope_cs=self.rope_table(capacity, device))
+        self._caches.add(cache)
+        return cache
+
+    def _paged_layer(self, module, key):
+        idx = getattr(module, "layer_idx", None)
+        for c in self._caches:
+            lyr = c.layer_of(idx, key)
+            if lyr is not None:
+                return lyr
+        return None
 
     def __call__(self, module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kwargs):
         b, hq, L, d = query.shape
-        S = key.shape[-2]
         if d != self.window.head_dim:
             raise ValueError(f"head_dim {d} != the tables' {self.window.head_dim}")
         scale = float(scaling) if scaling is not None else self.window.sm_scale
         windowed = self.mode == "win"
-        if L == 1:
-            # key/value [b, hkv, S, d]: one paged decode launch for the batch
-            kc, vc, table = I.pack_kv(key.transpose(1, 2), value.transpose(1, 2))
-            seq = torch.full((b,), S, dtype=torch.int32, device=query.device)
-            zhi = list(self.window.decode_zhi) if windowed else None
-            o = ops.decode_paged(query[:, :, 0, :], kc, vc, table, seq, S, zhi, scale, None, 0)
-            return o.view(b, 1, hq, d), None
+        lyr = self._paged_layer(module, key)
+        S = lyr.length if lyr is not None else key.shape[-2]
+        if S - 1 > self.window.n_ctx:
+            raise ValueError(f"context {S} exceeds the window tables' n_ctx {self.window.n_ctx}: rebuild them with "
+                             "a larger n_ctx")
         if L > S:
             raise ValueError(f"L>S invalid: L={L} S={S}")
+        if lyr is not None:
+            owner = lyr.owner
+            if (owner.rope_cs is not None) != self.rope_at_load:
+                raise ValueError("the cache was made for the other RoPE mode of this hook")
+            if L == 1:
+                zhi = list(self.window.decode_zhi) if windowed else None
+                o = ops.decode_paged(query[:, :, 0, :], lyr.k, lyr.v, owner.page_table, owner.seq_lens(S), S, zhi,
+                                     scale, owner.rope_cs, _lib.LAYOUT_HALF_SPLIT)
+                return o.view(b, 1, hq, d), None
+            zhi = list(self.window.prefill_zhi) if windowed else None
+            o, _ = ops.prefill(query.transpose(1, 2), lyr.k, lyr.v, owner.page_table, S, lyr.prev_length, zhi, scale,
+                               owner.rope_cs, _lib.LAYOUT_HALF_SPLIT)
+            return o, None  # [b, L, hq, d]
+        # any other cache: key/value hold the whole history [b, hkv, S, d]
+        rt = self.rope_table(S, query.device)
+        if L == 1:
+            kc, vc, table = I.pack_kv(key.transpose(1, 2), value.transpose(1, 2), rope=rt)
+            seq = torch.full((b,), S, dtype=torch.int32, device=query.device)
+            zhi = list(self.window.decode_zhi) if windowed else None
+            o = ops.decode_paged(query[:, :, 0, :], kc, vc, table, seq, S, zhi, scale, rt, 0)
+            return o.view(b, 1, hq, d), None
         zhi = self.window.prefill_zhi if windowed else None
         o, _ = I._flash_attn_fwd(query.transpose(1, 2), key.transpose(1, 2), value.transpose(1, 2), causal=True,
-                                 atflash_window_zhi=zhi, softmax_scale=scale)
+                                 atflash_window_zhi=zhi, softmax_scale=scale, rope=rt)
         return o, None  # [b, L, hq, d]
 
 
 def register(model, k_prefill: float = 2.0, k_decode: float = 2.0, n_ctx: int = None,
-             mode: str = "win") -> WindowAttention:
+             mode: str = "win", rope_at_load: bool = True) -> WindowAttention:
     """Build the tables from model.config, register the hook and switch the
     model's attention implementation to it.  Returns the hook (its .mode can be
-    changed between calls)."""
+    changed between calls; hook.new_cache(...) makes a bound PagedCache).
+    rope_at_load=True (default) replaces model.model.rotary_emb by
+    IdentityRotary, so the kernels apply RoPE; unregister() undoes that."""
     from transformers import AttentionInterface
     window = window_from_config(model.config, k_prefill, k_decode, n_ctx)
     scaling = getattr(getattr(model.model.layers[0], "self_attn", None), "scaling", None)
     if scaling is not None and abs(float(scaling) - window.sm_scale) > 1e-9:
         raise ValueError(f"attention scaling {scaling} != head_dim ** -0.5")
-    hook = WindowAttention(window, mode)
+    hook = WindowAttention(window, mode, rope_at_load)
+    rot = model.model.rotary_emb
+    if rope_at_load and not isinstance(rot, IdentityRotary):
+        model.model.rotary_emb = IdentityRotary(rot)
+    elif not rope_at_load and isinstance(rot, IdentityRotary):
+        model.model.rotary_emb = rot.original
     AttentionInterface.register(ATTN_NAME, hook)
     if hasattr(model, "set_attn_implementation"):
         model.set_attn_implementation(ATTN_NAME)
     else:
         model.config._attn_implementation = ATTN_NAME
     return hook
+
+
+def unregister(model, attn_implementation: str = "eager") -> None:
+    """Give the model back its own rotary embedding and the given attention."""
+    rot = model.model.rotary_emb
+    if isinstance(rot, IdentityRotary):
+        model.model.rotary_emb = rot.original
+    if hasattr(model, "set_attn_implementation"):
+        model.set_attn_implementation(attn_implementation)
+    else:
+        model.config._attn_implementation = attn_implementation

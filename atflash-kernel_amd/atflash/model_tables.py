@@ -101,9 +101,18 @@ class ModelWindow:
         return t * self.attention_scaling if self.attention_scaling != 1.0 else t
 
 
+# Default cap of the level tables: the reference's WIN_ZHI_CAP
+# (e2e_pipeline/atflash_e2e_fafi.py:55-58), above every context it runs (the 1M
+# series; Qwen2.5-7B-1M has max_position_embeddings 1,010,000).  A cap below a
+# call's longest causal distance would drop levels the rule keeps, and the
+# kernels refuse such a table.
+WIN_ZHI_CAP = 1_100_000
+
+
 def window_from_config(config, k_prefill: float = 2.0, k_decode: float = 2.0, n_ctx: int = None) -> ModelWindow:
-    """Tables for a HF config.  n_ctx caps the table (the longest context the
-    tables must describe; default: config.max_position_embeddings)."""
+    """Tables for a HF config.  n_ctx caps the table: the longest context the
+    tables must describe (default: the larger of WIN_ZHI_CAP and
+    config.max_position_embeddings)."""
     if float(getattr(config, "partial_rotary_factor", 1.0) or 1.0) != 1.0:
         raise ValueError("partial rotary embeddings are not supported by the window rule")
     d = head_dim_of(config)
@@ -112,7 +121,8 @@ def window_from_config(config, k_prefill: float = 2.0, k_decode: float = 2.0, n_
         raise ValueError(f"rotary class returned {inv.numel()} frequencies for head_dim {d}")
     check_pair_order(inv)
     base = raw_rope_base(config)
-    cap = int(n_ctx if n_ctx is not None else getattr(config, "max_position_embeddings", 1 << 20))
+    cap = int(n_ctx if n_ctx is not None else
+              max(WIN_ZHI_CAP, int(getattr(config, "max_position_embeddings", 0) or 0)))
     fz = tuple(AW.window_zhi_from_kret(d, base, float(k_prefill), cap))
     dz = tuple(AW.window_zhi_from_kret(d, base, float(k_decode), cap))
     return ModelWindow(head_dim=d, raw_base=base, k_prefill=float(k_prefill), k_decode=float(k_decode), n_ctx=cap,

@@ -37,7 +37,14 @@ bool aligned(const void* p, size_t n) { return (reinterpret_cast<uintptr_t>(p) %
 
 // Window table -> kernel argument.  NULL = window OFF (every level at every
 // distance).  Entries must be >= 0 and non-increasing, as zhi_table produces them.
-int make_table(const int32_t* zhi, atf::LevelTable* t) {
+// zhi[0] is the table's cap (D_eff >= 16 at every distance, so level 0 always
+// reaches it, window_tables/atflash_window.py:85-108): a level whose true width
+// exceeds the cap carries the cap instead, and would be dropped past it.  The
+// cap must therefore cover the longest causal distance of the call
+// (`longest`; the reference sets WIN_ZHI_CAP above every context it runs,
+// e2e_pipeline/atflash_e2e_fafi.py:55-58); a shorter cap is refused rather than
+// trimming levels the rule keeps.  longest < 0 skips the check.
+int make_table(const int32_t* zhi, atf::LevelTable* t, int64_t longest) {
   for (int i = 0; i < atf::kLevels; ++i) t->zhi[i] = zhi ? zhi[i] : INT32_MAX;
   if (!zhi) return ATF_OK;
   for (int i = 0; i < atf::kLevels; ++i) {
@@ -46,6 +53,11 @@ int make_table(const int32_t* zhi, atf::LevelTable* t) {
       return fail(ATF_ERR_INVALID, "zhi must be non-increasing (zhi[%d]=%d > zhi[%d]=%d)", i, zhi[i], i - 1,
                   zhi[i - 1]);
   }
+  if (longest >= 0 && zhi[0] < longest)
+    return fail(ATF_ERR_INVALID,
+                "window table cap zhi[0] = %d is below the longest causal distance %lld of this call; build the "
+                "table with n_ctx >= the context length",
+                zhi[0], static_cast<long long>(longest));
   return ATF_OK;
 }
 
@@ -151,7 +163,7 @@ int atf_prefill_bf16(void* out, int64_t o_sb, int64_t o_st, int64_t o_sh, float*
   if (q_sb % 8 || q_st % 8 || q_sh % 8) return fail(ATF_ERR_INVALID, "q strides must be multiples of 8 elements");
   if (o_sb % 4 || o_st % 4 || o_sh % 4) return fail(ATF_ERR_INVALID, "out strides must be multiples of 4 elements");
   atf::PrefillArgs a{};
-  if (int r = make_table(zhi, &a.lt)) return r;
+  if (int r = make_table(zhi, &a.lt, static_cast<int64_t>(nk) - 1)) return r;
   a.q = static_cast<const uint16_t*>(q);
   a.q_sb = q_sb; a.q_st = q_st; a.q_sh = q_sh;
   a.out = static_cast<uint16_t*>(out);
@@ -189,6 +201,11 @@ size_t atf_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, 
          static_cast<size_t>(batch) * num_kv_heads * ns * atf::kDecMaxGroup * (atf::kD + 2) * sizeof(float);
 }
 
+size_t atf_decode_counter_bytes(int batch, int num_kv_heads) {
+  if (batch <= 0 || num_kv_heads <= 0) return 0;
+  return counter_bytes(batch, num_kv_heads);
+}
+
 int atf_decode_paged_bf16(void* out, int64_t o_sb, int64_t o_sh, const void* q, int64_t q_sb, int64_t q_sh,
                           const void* k_cache, const void* v_cache, int num_pages, const int32_t* page_table,
                           int max_pages, const int32_t* seq_lens, int batch, int num_q_heads, int num_kv_heads,
@@ -219,7 +236,7 @@ int atf_decode_paged_bf16(void* out, int64_t o_sb, int64_t o_sh, const void* q, 
     return fail(ATF_ERR_WORKSPACE, "workspace of %zu bytes (16-byte aligned) required, got %zu", need,
                 workspace ? workspace_bytes : 0);
   atf::DecodeArgs a{};
-  if (int r = make_table(zhi, &a.lt)) return r;
+  if (int r = make_table(zhi, &a.lt, static_cast<int64_t>(max_seq_len) - 1)) return r;
   int ns = 1, pps = 1;
   decode_split(batch, num_kv_heads, max_seq_len, &ns, &pps);
   a.q = static_cast<const uint16_t*>(q);
@@ -257,7 +274,7 @@ int atf_prefill_tile_levels(int32_t* out, int n_row_tiles, int n_kblocks, int q_
                             void* stream) {
   if (!out || n_row_tiles < 0 || n_kblocks < 0 || q_offset < 0) return fail(ATF_ERR_INVALID, "bad arguments");
   atf::LevelTable t{};
-  if (int r = make_table(zhi, &t)) return r;
+  if (int r = make_table(zhi, &t, -1)) return r;
   hipError_t e = atf::launch_prefill_tile_levels(out, n_row_tiles, n_kblocks, q_offset, t,
                                                  static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "tile levels launch");
@@ -267,7 +284,7 @@ int atf_prefill_tile_levels(int32_t* out, int n_row_tiles, int n_kblocks, int q_
 int atf_decode_page_levels(int32_t* out, int n_pages, int seq_len, const int32_t* zhi, void* stream) {
   if (!out || n_pages < 0 || seq_len < 0) return fail(ATF_ERR_INVALID, "bad arguments");
   atf::LevelTable t{};
-  if (int r = make_table(zhi, &t)) return r;
+  if (int r = make_table(zhi, &t, -1)) return r;
   hipError_t e = atf::launch_decode_page_levels(out, n_pages, seq_len, t, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "page levels launch");
   return ok();

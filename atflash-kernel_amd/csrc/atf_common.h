@@ -125,15 +125,6 @@ __device__ __forceinline__ u32x4 rope_half(const u32x4& x1v, const u32x4& x2v, c
   return pack8(y);
 }
 
-// 8 bf16 times `scale`, rounded back to bf16.
-__device__ __forceinline__ u32x4 scale8(const u32x4& xv, float scale) {
-  float x[8];
-  unpack8(xv, x);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) x[i] *= scale;
-  return pack8(x);
-}
-
 __device__ __forceinline__ u32x4 ldg16(const void* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }

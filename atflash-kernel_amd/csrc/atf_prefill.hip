@@ -23,11 +23,13 @@
 //   Per (wave, kb) the QK contraction runs over the first L = D_eff/16 levels
 //   only, and the workgroup copies only the levels its first wave needs, so the
 //   out-of-window K levels never enter LDS.  Q is rotated (RoPE) at load.
-//   Online softmax in log2 units with a lazily updated reference max m_ref: Q is
-//   scaled by sm_scale*log2(e) when it is loaded (rounded to bf16 once, as it is
-//   anyway after RoPE), and every QK chain starts from -m_ref (a register tuple
-//   used as the C operand of its first MFMA), so the MFMAs return S - m_ref and
-//   P = exp2 of the accumulator directly.  O and l are rescaled only when a
+//   Online softmax in log2 units with a lazily updated reference max m_ref.
+//   With RoPE at load, Q is scaled by sm_scale*log2(e) as it is rotated (rounded
+//   to bf16 once, as it is anyway after RoPE), and every QK chain starts from
+//   -m_ref (a register tuple used as the C operand of its first MFMA), so the
+//   MFMAs return S - m_ref and P = exp2 of the accumulator directly.  A
+//   pre-rotated bf16 Q is used unscaled and the scale multiplies the fp32
+//   scores instead (kernel template kRaw).  O and l are rescaled only when a
 //   row's max grows past m_ref by more than 8, so P <= 256.
 #include "atf_launch.h"
 
@@ -372,8 +374,10 @@ __device__ __forceinline__ void qk_stream(const lds_u8* kb, bf16x8 (&f)[kRing], 
 }
 
 // P = exp2(S) of a tile pair packed to bf16 (Pf[p] is the B operand of the PV
-// steps of page p), and the lane's partial row sum of P.
-__device__ __forceinline__ float exp_tiles(const f32x16 (&S)[4], bf16x8 (&Pf)[8]) {
+// steps of page p), and the lane's partial row sum of P.  kRaw: S is in raw
+// score units (Q was not scaled) and P = exp2(S * c).
+template <bool kRaw>
+__device__ __forceinline__ float exp_tiles(const f32x16 (&S)[4], bf16x8 (&Pf)[8], float c) {
   float lt = 0.f;
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
@@ -382,8 +386,9 @@ __device__ __forceinline__ float exp_tiles(const f32x16 (&S)[4], bf16x8 (&Pf)[8]
       u32x4 pk;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float p0 = fast_exp2(S[kb][8 * hs + 2 * i]);
-        const float p1 = fast_exp2(S[kb][8 * hs + 2 * i + 1]);
+        const float s0 = S[kb][8 * hs + 2 * i], s1 = S[kb][8 * hs + 2 * i + 1];
+        const float p0 = fast_exp2(kRaw ? s0 * c : s0);
+        const float p1 = fast_exp2(kRaw ? s1 * c : s1);
         pk[i] = pack_bf16x2(p0, p1);
         lt += p0 + p1;
       }
@@ -393,6 +398,14 @@ __device__ __forceinline__ float exp_tiles(const f32x16 (&S)[4], bf16x8 (&Pf)[8]
   return lt;
 }
 
+// kRaw selects how the softmax scale c = sm_scale * log2(e) is applied.
+//   false (RoPE at load): Q is rotated and multiplied by c in fp32 and rounded
+//         to bf16 once, so the MFMAs return scores in log2 units directly;
+//   true  (pre-rotated bf16 Q): Q is used exactly as given and c multiplies the
+//         fp32 scores in the softmax (one multiply per score).  Scaling an
+//         already-rounded bf16 Q and rounding it again would add a second
+//         rounding error to every score, which grows with the score magnitude.
+template <bool kRaw>
 __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
   lds_u8* smem = (lds_u8*)(smem_raw);
@@ -446,7 +459,7 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
           load_cs8(a.rope_cs, a.q_offset + row, c0, cs);
           v = rope_half(ldg16(qrow + c0), ldg16(qrow + c1), cs, second, a.scale_log2);
         } else {
-          v = scale8(ldg16(qrow + (second ? c1 : c0)), a.scale_log2);
+          v = ldg16(qrow + (second ? c1 : c0));
         }
       }
       Qf[l] = v;
@@ -459,7 +472,9 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
   const float NEG_INF = -__builtin_huge_valf();
   float m_ref = 0.f;      // reference max (log2 units), set by the first tile
   float l_run = 0.f;      // this lane's partial row sum relative to m_ref
-  f32x16 Cm = f32x16{};   // -m_ref in every element
+  f32x16 Cm = f32x16{};   // -m_ref in every element (-m_ref / c with kRaw)
+  const float c = a.scale_log2;
+  const float inv_c = 1.f / c;
   const int grp = wave >> 2;   // ping-pong group (waves w and w+4 share a SIMD)
   const int rank = wave & 3;   // 0..3 within the group: the page of a tile this wave copies
   const bool copies_v = grp == 1;
@@ -634,7 +649,7 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
       // max taken: where it exceeds m_ref by more than 8 (always on the first
       // pair), m_ref moves up to it, O and l are rescaled, and the pair's P is
       // computed again from the shifted scores (shift 0 for the other lanes).
-      float lt = exp_tiles(S, Pf);
+      float lt = exp_tiles<kRaw>(S, Pf, c);
       if (__builtin_amdgcn_ballot_w64((u == 0) || !(lt <= 256.f)) != 0) {
         float mx = NEG_INF;
 #pragma unroll
@@ -642,6 +657,7 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
 #pragma unroll
           for (int r = 0; r < 16; ++r) mx = fmaxf(mx, S[kb][r]);
         mx = pair_max(mx);
+        if (kRaw) mx *= c;  // log2 units
         const bool grow = (u == 0) || mx > kLazyRescaleLog2;
         if (__builtin_amdgcn_ballot_w64(grow) != 0) {
           const float delta = grow ? mx : 0.f;
@@ -653,12 +669,13 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
           }
           m_ref += delta;
 #pragma unroll
-          for (int i = 0; i < 16; ++i) Cm[i] = -m_ref;
+          for (int i = 0; i < 16; ++i) Cm[i] = kRaw ? -m_ref * inv_c : -m_ref;
+          const float dS = kRaw ? delta * inv_c : delta;
 #pragma unroll
           for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) S[kb][r] -= delta;
-          lt = exp_tiles(S, Pf);
+            for (int r = 0; r < 16; ++r) S[kb][r] -= dS;
+          lt = exp_tiles<kRaw>(S, Pf, c);
         }
       }
       l_run += lt;
@@ -712,13 +729,18 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t s) {
   if (a.nq <= 0 || a.batch <= 0) return hipSuccess;
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kPfLdsTotal);
-    if (e != hipSuccess) return e;
+    for (const void* f : {reinterpret_cast<const void*>(prefill_kernel<false>),
+                          reinterpret_cast<const void*>(prefill_kernel<true>)}) {
+      hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kPfLdsTotal);
+      if (e != hipSuccess) return e;
+    }
     attr_set = true;
   }
   const int blocks = a.batch * a.n_qgroups * a.hq * 8;
-  hipLaunchKernelGGL(prefill_kernel, dim3(blocks), dim3(kPfWaves * 64), kPfLdsTotal, s, a);
+  if (a.rope_cs != nullptr)
+    hipLaunchKernelGGL(prefill_kernel<false>, dim3(blocks), dim3(kPfWaves * 64), kPfLdsTotal, s, a);
+  else
+    hipLaunchKernelGGL(prefill_kernel<true>, dim3(blocks), dim3(kPfWaves * 64), kPfLdsTotal, s, a);
   return hipGetLastError();
 }
 

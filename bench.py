@@ -29,8 +29,9 @@ roofline  prefill attention kernel (MFMA bound): algorithmic FLOPs per launch
           writer in `roofline_kv_write` (K and V read and written once plus one
           RoPE table row per position).
 cpu_baseline  the oracle's fp32 banded reference (oracle/attention.py) on the
-          host cores, on a sample of 32-row query tiles of the same 128K prefill,
-          extrapolated to the whole prefill (cost is linear in the tile position).
+          host cores: configuration C1 (N = 2048, 4 q heads, window k = 2 and
+          OFF) measured, median of 5 calls; and, as a secondary figure, the 128K
+          bench prefill extrapolated from sampled 32-row query tiles.
 """
 import argparse
 import json
@@ -184,34 +185,72 @@ def slice_ratios(N):
     return out
 
 
-def cpu_baseline(N, samples=160):
-    """The oracle on host cores for `samples` 32-row tiles spread over the 128K
-    prefill (window k = 2), extrapolated to all N/32 tiles."""
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(N, samples=64, calls=5):
+    """The oracle (oracle/attention.py, the fp32 banded restatement of
+    atflash/reference.py) on the host cores.
+
+    value: configuration C1 measured -- B = 1, Hq = 4, Hkv = 1, d = 128,
+    N = 2048, RoPE base 1e4 (pre-rotated inputs), fp32 N(0,1) from seed 0, window
+    k = 2 -- the median of `calls` calls after one warm-up; the same for window
+    OFF in value_off.  Threads: the box's CPU share for one GPU (torch's thread
+    count, which follows OMP_NUM_THREADS there).
+    extrapolated_128k: the bench workload (Qwen2.5-7B shape, 128K, k = 2) from
+    `samples` sampled 32-row query tiles, mean tile time x N/32 tiles plus the
+    per-call work scaled to N."""
     import torch
     from oracle import attention as OA
     from oracle import window_rule as WR
-    threads = min(16, os.cpu_count() or 1)
-    torch.set_num_threads(threads)
+    threads = torch.get_num_threads()
     g = torch.Generator().manual_seed(0)
+    q = torch.randn((1, 4, 2048, D), generator=g)
+    k = torch.randn((1, 1, 2048, D), generator=g)
+    v = torch.randn((1, 1, 2048, D), generator=g)
+    res = {}
+    for name, k_ret in (("k2", 2.0), ("off", float("inf"))):
+        w = WR.wavelengths_sorted(D, 1e4, k_ret)
+        ts = []
+        for i in range(calls + 1):
+            t0 = time.perf_counter()
+            OA.ref_window_attn(q, k, v, w, phase="prefill", block_m=32, block_n=32)
+            if i:
+                ts.append((time.perf_counter() - t0) * 1e3)
+        res[name] = statistics.median(ts)
+
+    # secondary: the 128K bench workload, sampled
     w = WR.wavelengths_sorted(D, BASE, 2.0)
     rows = [int(((i + 0.5) / samples) * N) // 32 * 32 for i in range(samples)]
     hi = max(rows) + 32
     q = torch.randn((1, HQ, N, D), generator=g)
     k = torch.randn((1, HKV, hi, D), generator=g)
     v = torch.randn((1, HKV, hi, D), generator=g)
+
     def run(tiles):
         t0 = time.perf_counter()
         OA.ref_window_attn(q[:, :, :hi], k, v, w, phase="prefill", block_m=32, block_n=32, tile_rows=tiles)
         return time.perf_counter() - t0
-    fixed = run([])            # per-call work independent of the tiles (GQA expand, casts)
+    fixed = min(run([]), run([]))
     sampled = run(rows)
     per_tile = max(0.0, sampled - fixed) / samples
-    est_s = fixed * (N / hi) + per_tile * (N / 32)
-    return {"value": est_s * 1e3, "unit": "ms", "cores": threads, "kind": "port",
-            "sample": f"oracle fp32 ref_window_attn (window k=2, tiles 32x32) on {samples} 32-row query tiles at "
-                      f"rows {rows} of the {N}-token Qwen2.5-7B-shape prefill; mean tile time x {N // 32} tiles "
-                      f"+ the per-call GQA expand scaled to N; CPU seconds measured {fixed + sampled:.1f}",
-            "per_tile_s": per_tile, "fixed_s": fixed}
+    est_ms = (fixed * (N / hi) + per_tile * (N / 32)) * 1e3
+    return {"value": res["k2"], "unit": "ms", "cores": threads, "kind": "port",
+            "value_off": res["off"], "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count(),
+            "sample": f"C1: oracle fp32 ref_window_attn, B=1 Hq=4 Hkv=1 d=128 N=2048, base 1e4, seed 0, tiles (32, 32); "
+                      f"median of {calls} calls after 1 warm-up; value = window k=2, value_off = window OFF",
+            "extrapolated_128k": {"value": est_ms, "unit": "ms",
+                                  "sample": f"Qwen2.5-7B-shape 128K prefill, window k=2: {samples} sampled 32-row "
+                                            f"tiles x {N // 32} tiles + per-call work scaled to N",
+                                  "per_tile_s": per_tile, "fixed_s": fixed}}
 
 
 def main():

@@ -10,8 +10,10 @@
  *
  * Window tables.  `zhi` is a HOST array of ATF_LEVELS int32 entries: zhi[i] is
  * the largest causal key distance at which 16-dim level i is still read
- * (window_tables/atflash_window.py:85-108, capped at a value >= the longest
- * causal distance of the call).  NULL means window OFF: plain causal attention,
+ * (window_tables/atflash_window.py:85-108).  zhi[0] is the table's cap and must
+ * be >= the longest causal distance of the call (prefill nk - 1, decode
+ * max_seq_len - 1); a smaller cap is refused with ATF_ERR_INVALID, since it
+ * would drop levels the rule keeps.  NULL means window OFF: plain causal attention,
  * every level read at every distance.  Level l holds RoPE pairs
  * r in [64-8(l+1), 64-8l) (dims r and r+64 of the half-split layout).
  *
@@ -67,6 +69,14 @@ const char* atf_last_error(void);
  * page_table[b][pos / 16], slot pos % 16.  K is rotated with rope_cs at that
  * position.  Source strides are in elements; the last dim is contiguous.
  *
+ * Positions live in device memory (start_pos), so they are checked in the
+ * kernel, not here, and a token that cannot be placed is SKIPPED without an
+ * error: a negative position, a position at or past rope_max_pos (when rope_cs
+ * is given), a page index pos / 16 at or past max_pages, or a page-table entry
+ * outside [0, num_pages).  Attention over such a token would read whatever the
+ * slot held before, so callers must keep positions inside the page table and
+ * the RoPE table (atflash.cache.PagedKVCache checks this on the host).
+ *
  * Replaces the reference's RoPE + head-dim permutation patch and HF cache append
  * (e2e_pipeline/atflash_e2e_fafi.py:186-192, 101-119).
  */
@@ -99,14 +109,21 @@ int atf_prefill_bf16(void* out, int64_t o_sb, int64_t o_st, int64_t o_sh, float*
                      int layout, void* stream);
 
 /*
- * Bytes of device workspace atf_decode_paged_bf16 needs for these sizes: split
- * partials plus one arrival counter per (sequence, kv head).  The workspace
- * must be zero-filled once before its first use; every completed call leaves
- * its counters at zero again, so the same buffer serves later calls of any
- * size up to the one it was sized for.  Calls that share a workspace must be
- * ordered on one stream (concurrent calls on one workspace race).
+ * Bytes of device workspace atf_decode_paged_bf16 needs for these sizes: an
+ * arrival-counter region (one uint32 per (sequence, kv head), padded to 256 B)
+ * at the start of the workspace, followed by the split partials.
+ *
+ * Zero rule: the first atf_decode_counter_bytes(batch, num_kv_heads) bytes of
+ * the workspace must be zero when a call starts.  A completed call leaves
+ * exactly that many leading bytes at zero; the bytes after them hold split
+ * partials.  So a workspace zero-filled once serves any later call whose
+ * counter region is no larger than the previous call's; before a call with a
+ * larger batch * num_kv_heads, zero its counter region again (a call only
+ * writes partials past its own counter region).  Calls that share a workspace
+ * must be ordered on one stream (concurrent calls on one workspace race).
  */
 size_t atf_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int max_seq_len);
+size_t atf_decode_counter_bytes(int batch, int num_kv_heads);
 
 /*
  * Windowed split-KV decode: one query token per sequence at position

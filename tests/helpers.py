@@ -36,9 +36,18 @@ def rotate(x_bshd, positions, base):
     return OA.rope_hf(xt, positions, inv).transpose(1, 2)
 
 
-def prefill_oracle(q, k, v, base, k_ret, rope, q_offset=0, tile_rows=None, mode="fp32"):
+def wvec_for_levels(zhi):
+    """Sorted widths whose window rule reproduces a given level table exactly:
+    the 8 pairs of level i all get width zhi[i], so n_active(z) =
+    8 * #{i : zhi[i] >= z} and D_eff(z) = 16 * #{i : zhi[i] >= z} (clamped to
+    >= 16), the identity the kernels use."""
+    return [float(z) for z in zhi for _ in range(8)]
+
+
+def prefill_oracle(q, k, v, base, k_ret, rope, q_offset=0, tile_rows=None, mode="fp32", widths=None):
     """fp32 oracle of the prefill kernel: optional RoPE (fp32), sorted-pair layout,
-    tiles (32, 32).  q [B, Nq, Hq, D] and k, v [B, Nk, Hkv, D] bf16, half-split."""
+    tiles (32, 32).  q [B, Nq, Hq, D] and k, v [B, Nk, Hkv, D] bf16, half-split.
+    `widths` (sorted pair widths) overrides the table of (base, k_ret)."""
     Nq, Nk = q.shape[1], k.shape[1]
     if rope:
         qr = rotate(q, torch.arange(q_offset, q_offset + Nq), base)
@@ -50,7 +59,8 @@ def prefill_oracle(q, k, v, base, k_ret, rope, q_offset=0, tile_rows=None, mode=
     vs = v.float().transpose(1, 2)
     if mode == "bf16":
         qs, ks, vs = qs.to(BF), ks.to(BF), vs.to(BF)
-    o = OA.ref_window_attn(qs, ks, vs, wvec(base, k_ret), phase="prefill", block_m=PREFILL_BM,
+    o = OA.ref_window_attn(qs, ks, vs, wvec(base, k_ret) if widths is None else widths, phase="prefill",
+                           block_m=PREFILL_BM,
                            block_n=PREFILL_BN, q_offset=q_offset, tile_rows=tile_rows, mode=mode)
     return o.float().transpose(1, 2)  # B Nq Hq D
 
@@ -80,3 +90,37 @@ def assert_close(out, ref, what=""):
     assert math.isfinite(mx), f"{what}: non-finite output"
     assert mx <= TOL_MAX and mean <= TOL_MEAN, f"{what}: max {mx:.3e} (tol {TOL_MAX}) mean {mean:.3e} (tol {TOL_MEAN})"
     return mx, mean
+
+
+def gpu_qkv(B, N, hq, hkv, dev, seed, nq=None):
+    """bf16 N(0,1) q [B, Nq, Hq, D], k, v [B, N, Hkv, D] generated on the GPU
+    (fp32 from a seeded device generator, then cast), for sizes where CPU
+    generation would dominate the test."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    shapes = ((B, N if nq is None else nq, hq, D), (B, N, hkv, D), (B, N, hkv, D))
+    return tuple(torch.randn(s, generator=g, device=dev, dtype=torch.float32).to(BF) for s in shapes)
+
+
+def prefill_oracle_rows(q_rows, k, v, base, k_ret, rows, rope=True):
+    """fp32 oracle of 32-row query tiles of a long single-shot prefill.
+
+    q_rows: {r: q[:, r:r+32] bf16 CPU}; k, v: [B, >= max(rows)+32, Hkv, D] bf16
+    CPU (half-split).  K is rotated and permuted once; each tile is evaluated
+    with its own keys 0..r+31 and q_offset = r, so its (32, 32) tile grid is the
+    kernel's (r a multiple of 32).  Returns {r: [B, 32, Hq, D] fp32}."""
+    hi = max(rows) + PREFILL_BM
+    kr = rotate(k[:, :hi], torch.arange(hi), base) if rope else k[:, :hi].float()
+    ks = OA.to_sorted(kr).transpose(1, 2).contiguous()
+    vs = v[:, :hi].float().transpose(1, 2).contiguous()
+    w = wvec(base, k_ret)
+    out = {}
+    for r in rows:
+        assert r % PREFILL_BM == 0
+        qt = q_rows[r]
+        qr = rotate(qt, torch.arange(r, r + qt.shape[1]), base) if rope else qt.float()
+        qs = OA.to_sorted(qr).transpose(1, 2)
+        n = r + qt.shape[1]
+        o = OA.ref_window_attn(qs, ks[:, :, :n], vs[:, :, :n], w, phase="prefill", block_m=PREFILL_BM,
+                               block_n=PREFILL_BN, q_offset=r)
+        out[r] = o.transpose(1, 2)
+    return out

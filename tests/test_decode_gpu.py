@@ -150,6 +150,44 @@ def test_workspace_reuse_across_calls(dev):
     H.assert_close(s, H.decode_oracle(*small, 1e4, float("inf"), False), "small call between large ones")
 
 
+def test_workspace_reuse_with_more_sequences_and_heads(dev):
+    """A call whose counter region (one uint32 per sequence x kv head) is larger
+    than the previous call's reuses the cached workspace: B = 1 x 4 kv heads at
+    20K tokens (256 B of counters, then partials), then B = 32 x 4 kv heads at
+    300 tokens (512 B of counters over the first call's partials), then the
+    first again.  Every output is checked against the oracle."""
+    from atflash import interface, ops
+    from atflash.cache import PagedKVCache
+    hq, hkv, base = 28, 4, 1e7
+
+    def run(lens, seed):
+        B = len(lens)
+        cache = PagedKVCache(sum(-(-n // 16) for n in lens) + 3, hkv, dev)
+        g = torch.Generator().manual_seed(seed)
+        seqs = []
+        for b, n in enumerate(lens):
+            cache.add_sequence(b, n)
+            seqs.append((H.randn_bf16((1, n, hkv, H.D), g), H.randn_bf16((1, n, hkv, H.D), g)))
+        table = cache.page_table(list(range(B)))
+        for b, (k, v) in enumerate(seqs):
+            torch.ops.atflash.kv_write(cache.k, cache.v, k.to(dev), v.to(dev),
+                                       torch.zeros(1, dtype=torch.int32, device=dev), table[b:b + 1].contiguous(),
+                                       None, 0)
+        q = H.randn_bf16((B, hq, H.D), g)
+        out = interface.decode_paged(q.to(dev), cache, table, torch.tensor(lens, dtype=torch.int32, device=dev),
+                                     max(lens)).cpu()
+        for b, (k, v) in enumerate(seqs):
+            H.assert_close(out[b], H.decode_oracle(q[b], k[0], v[0], base, float("inf"), False),
+                           f"B={B} seq {b} len {lens[b]}")
+        return out
+
+    ops._DECODE_WS.clear()
+    first = run([20000], 31)
+    run([300] * 32, 32)
+    again = run([20000], 31)
+    assert torch.equal(first, again)
+
+
 def test_split_count_cap_long_sequence(dev):
     """One kv head and 70000 tokens: the split count hits its cap (256 splits)."""
     g = torch.Generator().manual_seed(22)

@@ -5,7 +5,14 @@ random-init Qwen2 model (2 layers, head_dim 128, GQA 4/2, RoPE base 1e4).
 * window on (k = 2): the hook's logits equal those of the same model whose
   attention is the fp32 oracle (oracle/attention.py, registered through the same
   AttentionInterface), for a 300-token prefill and for one decode step against
-  the model's own KV cache (the L == 1 path).
+  HF's own KV cache (the L == 1 path, history re-packed per call);
+* the serving path, atflash.hf.PagedCache: chunked prefill into the paged cache
+  and several decode steps against it equal the oracle model step by step, and
+  (gate C0 at model level, gates/c0_chunk_neutrality.py:22-61) a chunked prefill
+  through the whole model equals the single-shot one on the last logits and on
+  layer 0's cached keys;
+* both RoPE modes of the hook: RoPE at load (the kernels rotate Q and K) and
+  HF's rotation (pre-rotated q and k).
 """
 import pytest
 import torch
@@ -90,3 +97,77 @@ def test_hook_window_on_equals_oracle_prefill_and_decode(dev):
     hook.mode = "off"
     off = _logits(model, ids)
     assert (off - got_pf).abs().max().item() > 0.05
+
+
+def _paged_run(model, hook, ids, chunk, steps, dev):
+    """Prefill ids in chunks through a PagedCache, then `steps` decode steps
+    feeding the given continuation.  Returns (prefill last logits, [step logits],
+    cache)."""
+    T = ids.shape[1] - steps
+    cache = hook.new_cache(model.config, ids.shape[0], ids.shape[1] + 8, dev)
+    with torch.no_grad():
+        for c0 in range(0, T, chunk):
+            out = model(ids[:, c0:min(T, c0 + chunk)], past_key_values=cache, use_cache=True, logits_to_keep=1)
+        last = out.logits[:, -1].float()
+        dec = []
+        for t in range(T, ids.shape[1]):
+            out = model(ids[:, t:t + 1], past_key_values=cache, use_cache=True)
+            dec.append(out.logits[:, -1].float())
+    return last, dec, cache
+
+
+def _oracle_steps(model, ids, steps):
+    """The same sequence through HF's DynamicCache with the oracle attention."""
+    T = ids.shape[1] - steps
+    with torch.no_grad():
+        out = model(ids[:, :T], use_cache=True)
+        last = out.logits[:, -1].float()
+        pkv = out.past_key_values
+        dec = []
+        for t in range(T, ids.shape[1]):
+            out = model(ids[:, t:t + 1], past_key_values=pkv, use_cache=True)
+            pkv = out.past_key_values
+            dec.append(out.logits[:, -1].float())
+    return last, dec
+
+
+@pytest.mark.parametrize("rope_at_load", [True, False])
+def test_paged_cache_chunked_prefill_and_decode_equal_oracle(rope_at_load, dev):
+    model = _model(dev)
+    steps = 4
+    ids = torch.randint(0, 512, (1, 640 + steps), generator=torch.Generator().manual_seed(3)).to(dev)
+    AttentionInterface.register("atf_oracle", _oracle_attention)
+    model.set_attn_implementation("atf_oracle")
+    ref_last, ref_dec = _oracle_steps(model, ids, steps)
+    hook = hf.register(model, K_RET, K_RET, n_ctx=4096, mode="win", rope_at_load=rope_at_load)
+    assert isinstance(model.model.rotary_emb, hf.IdentityRotary) == rope_at_load
+    last, dec, cache = _paged_run(model, hook, ids, 128, steps, dev)
+    assert cache.get_seq_length() == ids.shape[1]
+    _close(last, ref_last, f"paged cache, rope_at_load={rope_at_load}: prefill in 128-token chunks")
+    for i, (a, b) in enumerate(zip(dec, ref_dec)):
+        _close(a, b, f"paged cache, rope_at_load={rope_at_load}: decode step {i}")
+    hf.unregister(model)
+    assert not isinstance(model.model.rotary_emb, hf.IdentityRotary)
+
+
+@pytest.mark.parametrize("mode", ["win", "off"])
+def test_model_chunked_prefill_equals_single_shot(mode, dev):
+    """Gate C0 through the whole model with the paged cache: 2048 tokens in one
+    forward against chunks of 512 (chunk starts are multiples of the 32-row tile,
+    so the window's tiles coincide).  The attention kernels are chunk-neutral bit
+    for bit, and on this software stack the projections (GEMMs of 2048 and of
+    512 rows) are too: the last logits and layer 0's cached keys are equal bit
+    for bit, as the reference's gate reports for its stack."""
+    model = _model(dev)
+    hook = hf.register(model, K_RET, K_RET, n_ctx=4096, mode=mode)
+    ids = torch.randint(0, 512, (1, 2048), generator=torch.Generator().manual_seed(4)).to(dev)
+    single, _, c1 = _paged_run(model, hook, ids, 2048, 0, dev)
+    chunked, _, c2 = _paged_run(model, hook, ids, 512, 0, dev)
+    k1 = c1.layers[0].k[:2048 // 16]
+    k2 = c2.layers[0].k[:2048 // 16]
+    kd = (k1.float() - k2.float()).abs().max().item()
+    ld = (single - chunked).abs().max().item()
+    print(f"[C0 model] {mode}: last logits bitwise {torch.equal(single, chunked)} max|d| {ld:.3e}; "
+          f"layer-0 K bitwise {torch.equal(k1, k2)} max|d| {kd:.3e}", flush=True)
+    assert torch.equal(single, chunked) and torch.equal(k1, k2)
+    hf.unregister(model)

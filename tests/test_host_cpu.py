@@ -189,6 +189,41 @@ def test_validation_status_codes():
     assert L.atf_decode_page_levels(None, 4, 64, None, None) == INV
 
 
+def test_table_cap_below_longest_distance_is_refused():
+    """zhi[0] is the table's cap; a cap below the call's longest causal distance
+    would drop levels the rule keeps (e2e_pipeline/atflash_e2e_fafi.py:55-58), so
+    the boundary refuses it.  The calls below stop at that check (the pointers
+    are never used)."""
+    from atflash import atflash_window as AW
+    _lib = _lib_or_skip()
+    L = _lib.lib()
+    INV = _lib.ATF_ERR_INVALID
+    short = (ctypes.c_int32 * 8)(*AW.window_zhi_from_kret(128, 1e7, 2.0, 126))   # cap 126 < nk - 1 = 127
+    assert short[0] == 126
+    assert _prefill(L, zhi=short) == INV
+    assert b"cap" in L.atf_last_error()
+    ws = L.atf_decode_workspace_bytes(1, 28, 4, 128)
+    assert _decode(L, zhi=short, ws_bytes=ws) == INV                   # max_seq_len 128: longest 127
+    assert b"cap" in L.atf_last_error()
+    inf_short = (ctypes.c_int32 * 8)(*([100] * 8))                     # k = inf capped at 100
+    assert _decode(L, zhi=inf_short, ws_bytes=ws, max_seq_len=102) == INV
+
+
+def test_counter_region_size():
+    """The arrival-counter region at the start of the decode workspace: one
+    uint32 per (sequence, kv head), padded to 256 bytes."""
+    _lib = _lib_or_skip()
+    L = _lib.lib()
+    assert L.atf_decode_counter_bytes(0, 4) == 0
+    assert L.atf_decode_counter_bytes(1, 4) == 256
+    assert L.atf_decode_counter_bytes(64, 1) == 256
+    assert L.atf_decode_counter_bytes(65, 1) == 512
+    assert L.atf_decode_counter_bytes(32, 8) == 1024
+    for b, hkv, n in [(1, 4, 131072), (32, 4, 300), (8, 8, 163840)]:
+        c = L.atf_decode_counter_bytes(b, hkv)
+        assert (L.atf_decode_workspace_bytes(b, 28, hkv, n) - c) % (16 * 130 * 4) == 0
+
+
 # ---------------------------------------------------------------- Python operators
 
 def test_ops_refuse_cpu_tensors_and_bad_tables():

@@ -266,13 +266,19 @@ def test_no_dot_result_hazards(kernel_asm):
         assert dot_hazards(asm) == [], name
 
 
+# the two instantiations of the prefill kernel: scores scaled through Q (RoPE at
+# load) and raw scores scaled in the softmax (pre-rotated Q)
+PREFILL_KERNELS = ("_ZN3atf14prefill_kernelILb0EEEvNS_11PrefillArgsE", "_ZN3atf14prefill_kernelILb1EEEvNS_11PrefillArgsE")
+
+
 def test_prefill_kernel_does_not_spill(kernel_asm):
     asm = kernel_asm["atf_prefill.hip"]
     # kernel metadata: one "- .agpr_count" block per kernel, holding .name and .vgpr_spill_count
-    blocks = [b for b in asm.split("  - .agpr_count:") if re.search(r"\.name:\s+_ZN3atf14prefill_kernel", b)]
-    assert len(blocks) == 1, "prefill_kernel metadata not found"
-    spill = re.search(r"\.vgpr_spill_count:\s+(\d+)", blocks[0])
-    assert spill and int(spill.group(1)) == 0
+    for name in PREFILL_KERNELS:
+        blocks = [b for b in asm.split("  - .agpr_count:") if re.search(r"\.name:\s+" + name + r"\s", b)]
+        assert len(blocks) == 1, f"{name} metadata not found"
+        spill = re.search(r"\.vgpr_spill_count:\s+(\d+)", blocks[0])
+        assert spill and int(spill.group(1)) == 0, name
 
 
 def pipelined_runs(waits, depth=3):
@@ -294,8 +300,9 @@ def test_prefill_operand_ring_keeps_lds_reads_in_flight(kernel_asm):
     # the PV stream of a tile pair (32 MFMAs) and the 8-level QK stream of its
     # four 32-key blocks (32 MFMAs, the ring draining over the last three) run
     # with the operand reads of several later MFMAs still outstanding
-    waits = lds_waits_before_mfma(kernel_asm["atf_prefill.hip"], "_ZN3atf14prefill_kernelENS_11PrefillArgsE")
-    assert len(waits) >= 64
-    runs = sorted(pipelined_runs(waits), reverse=True)
-    assert runs[0] >= 31, runs
-    assert len(runs) >= 2 and runs[1] >= 25, runs
+    for name in PREFILL_KERNELS:
+        waits = lds_waits_before_mfma(kernel_asm["atf_prefill.hip"], name)
+        assert len(waits) >= 64, name
+        runs = sorted(pipelined_runs(waits), reverse=True)
+        assert runs[0] >= 31, (name, runs)
+        assert len(runs) >= 2 and runs[1] >= 25, (name, runs)

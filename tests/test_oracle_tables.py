@@ -148,3 +148,23 @@ def test_deff_segments_cover_keys_with_tile_deff(phase):
             assert per_key[m] == WR.deff_of_zmin(z, w, d)
         # adjacent segments differ (maximal runs)
         assert all(segs[i][2] != segs[i + 1][2] for i in range(len(segs) - 1))
+
+
+def test_widths_for_a_level_table_reproduce_it():
+    """tests/helpers.wvec_for_levels: widths that make the oracle's rule
+    reproduce a given level table.  The oracle's own zhi_table of those widths
+    returns the table (up to the cap), and D_eff agrees with the identity
+    D_eff(z) = 16 * #{i : zhi[i] >= z} at every distance; for a table made by the
+    RoPE rule the constructed widths give the same tile D_eff as the real ones."""
+    import helpers as H
+    for zhi in [(4096, 700, 300, 150, 90, 40, 10, 0), (4096, 4096, 1000, 1000, 999, 5, 0, 0),
+                tuple(WR.window_zhi_from_kret(128, 1e4, 0.5, 8192))]:
+        w = H.wvec_for_levels(zhi)
+        assert len(w) == 64 and all(a >= b for a, b in zip(w, w[1:]))
+        assert tuple(WR.zhi_table(w, 128, zhi[0])) == tuple(zhi)
+        for z in range(0, 5000, 7):
+            assert WR.deff_of_zmin(z, w, 128) == 16 * WR.levels_of_zmin(z, zhi)
+    real = WR.wavelengths_sorted(128, 1e4, 0.5)
+    built = H.wvec_for_levels(WR.window_zhi_from_kret(128, 1e4, 0.5, 8192))
+    for z in range(0, 8192, 3):
+        assert WR.deff_of_zmin(z, real, 128) == WR.deff_of_zmin(z, built, 128)
