@@ -206,13 +206,17 @@ size_t atf_decode_counter_bytes(int batch, int num_kv_heads) {
   return counter_bytes(batch, num_kv_heads);
 }
 
-int atf_decode_paged_bf16(void* out, int64_t o_sb, int64_t o_sh, const void* q, int64_t q_sb, int64_t q_sh,
-                          const void* k_cache, const void* v_cache, int num_pages, const int32_t* page_table,
-                          int max_pages, const int32_t* seq_lens, int batch, int num_q_heads, int num_kv_heads,
-                          int max_seq_len, const int32_t* zhi, float sm_scale, const float* rope_cs,
-                          int rope_max_pos, int layout, void* workspace, size_t workspace_bytes, void* stream) {
-  if (batch < 0) return fail(ATF_ERR_INVALID, "batch must be >= 0");
-  if (batch == 0) return ok();
+}  // extern "C"
+
+namespace {
+
+// Validation and argument packing shared by the two decode entry points
+// (everything except the workspace).
+int decode_prepare(void* out, int64_t o_sb, int64_t o_sh, const void* q, int64_t q_sb, int64_t q_sh,
+                   const void* k_cache, const void* v_cache, int num_pages, const int32_t* page_table, int max_pages,
+                   const int32_t* seq_lens, int batch, int num_q_heads, int num_kv_heads, int max_seq_len,
+                   const int32_t* zhi, float sm_scale, const float* rope_cs, int rope_max_pos, int layout,
+                   atf::DecodeArgs* a) {
   if (!out || !q || !k_cache || !v_cache || !page_table || !seq_lens)
     return fail(ATF_ERR_INVALID, "null pointer argument");
   if (num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0)
@@ -231,42 +235,85 @@ int atf_decode_paged_bf16(void* out, int64_t o_sb, int64_t o_sh, const void* q, 
     return fail(ATF_ERR_INVALID, "q, caches must be 16-byte and out 8-byte aligned");
   if (q_sb % 8 || q_sh % 8) return fail(ATF_ERR_INVALID, "q strides must be multiples of 8 elements");
   if (o_sb % 4 || o_sh % 4) return fail(ATF_ERR_INVALID, "out strides must be multiples of 4 elements");
+  if (int r = make_table(zhi, &a->lt, static_cast<int64_t>(max_seq_len) - 1)) return r;
+  int ns = 1, pps = 1;
+  decode_split(batch, num_kv_heads, max_seq_len, &ns, &pps);
+  a->q = static_cast<const uint16_t*>(q);
+  a->q_sb = q_sb;
+  a->q_sh = q_sh;
+  a->k_cache = static_cast<const uint16_t*>(k_cache);
+  a->v_cache = static_cast<const uint16_t*>(v_cache);
+  a->num_pages = num_pages;
+  a->page_table = page_table;
+  a->max_pages = max_pages;
+  a->seq_lens = seq_lens;
+  a->max_seq_len = max_seq_len;
+  a->batch = batch;
+  a->hq = num_q_heads;
+  a->hkv = num_kv_heads;
+  a->group = num_q_heads / num_kv_heads;
+  a->n_splits = ns;
+  a->pages_per_split = pps;
+  a->scale_log2 = sm_scale * 1.4426950408889634f;
+  a->rope_cs = rope_cs;
+  a->layout = layout;
+  a->out = static_cast<uint16_t*>(out);
+  a->o_sb = o_sb;
+  a->o_sh = o_sh;
+  return ATF_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int atf_decode_paged_bf16(void* out, int64_t o_sb, int64_t o_sh, const void* q, int64_t q_sb, int64_t q_sh,
+                          const void* k_cache, const void* v_cache, int num_pages, const int32_t* page_table,
+                          int max_pages, const int32_t* seq_lens, int batch, int num_q_heads, int num_kv_heads,
+                          int max_seq_len, const int32_t* zhi, float sm_scale, const float* rope_cs,
+                          int rope_max_pos, int layout, void* workspace, size_t workspace_bytes, void* stream) {
+  if (batch < 0) return fail(ATF_ERR_INVALID, "batch must be >= 0");
+  if (batch == 0) return ok();
+  atf::DecodeArgs a{};
+  if (int r = decode_prepare(out, o_sb, o_sh, q, q_sb, q_sh, k_cache, v_cache, num_pages, page_table, max_pages,
+                             seq_lens, batch, num_q_heads, num_kv_heads, max_seq_len, zhi, sm_scale, rope_cs,
+                             rope_max_pos, layout, &a))
+    return r;
   const size_t need = atf_decode_workspace_bytes(batch, num_q_heads, num_kv_heads, max_seq_len);
   if (!workspace || workspace_bytes < need || !aligned(workspace, 16))
     return fail(ATF_ERR_WORKSPACE, "workspace of %zu bytes (16-byte aligned) required, got %zu", need,
                 workspace ? workspace_bytes : 0);
-  atf::DecodeArgs a{};
-  if (int r = make_table(zhi, &a.lt, static_cast<int64_t>(max_seq_len) - 1)) return r;
-  int ns = 1, pps = 1;
-  decode_split(batch, num_kv_heads, max_seq_len, &ns, &pps);
-  a.q = static_cast<const uint16_t*>(q);
-  a.q_sb = q_sb;
-  a.q_sh = q_sh;
-  a.k_cache = static_cast<const uint16_t*>(k_cache);
-  a.v_cache = static_cast<const uint16_t*>(v_cache);
-  a.num_pages = num_pages;
-  a.page_table = page_table;
-  a.max_pages = max_pages;
-  a.seq_lens = seq_lens;
-  a.max_seq_len = max_seq_len;
-  a.batch = batch;
-  a.hq = num_q_heads;
-  a.hkv = num_kv_heads;
-  a.group = num_q_heads / num_kv_heads;
-  a.n_splits = ns;
-  a.pages_per_split = pps;
-  a.scale_log2 = sm_scale * 1.4426950408889634f;
-  a.rope_cs = rope_cs;
-  a.layout = layout;
-  a.out = static_cast<uint16_t*>(out);
-  a.o_sb = o_sb;
-  a.o_sh = o_sh;
   char* ws = static_cast<char*>(workspace);
   a.counters = reinterpret_cast<uint32_t*>(ws);
   a.ws_ml = reinterpret_cast<float*>(ws + counter_bytes(batch, num_kv_heads));
-  a.ws_o = a.ws_ml + static_cast<size_t>(batch) * num_kv_heads * ns * atf::kDecMaxGroup * 2;
+  a.ws_o = a.ws_ml + static_cast<size_t>(batch) * num_kv_heads * a.n_splits * atf::kDecMaxGroup * 2;
   hipError_t e = atf::launch_decode(a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "decode launch");
+  return ok();
+}
+
+int atf_decode_paged_bf16_noalloc(void* out, int64_t o_sb, int64_t o_sh, const void* q, int64_t q_sb, int64_t q_sh,
+                                  const void* k_cache, const void* v_cache, int num_pages,
+                                  const int32_t* page_table, int max_pages, const int32_t* seq_lens, int batch,
+                                  int num_q_heads, int num_kv_heads, int max_seq_len, const int32_t* zhi,
+                                  float sm_scale, const float* rope_cs, int rope_max_pos, int layout, void* stream) {
+  if (batch < 0) return fail(ATF_ERR_INVALID, "batch must be >= 0");
+  if (batch == 0) return ok();
+  atf::DecodeArgs a{};
+  if (int r = decode_prepare(out, o_sb, o_sh, q, q_sb, q_sh, k_cache, v_cache, num_pages, page_table, max_pages,
+                             seq_lens, batch, num_q_heads, num_kv_heads, max_seq_len, zhi, sm_scale, rope_cs,
+                             rope_max_pos, layout, &a))
+    return r;
+  const size_t pairs = static_cast<size_t>(batch) * num_kv_heads;
+  const size_t partial = pairs * a.n_splits * atf::kDecMaxGroup * (atf::kD + 2) * sizeof(float);
+  if (pairs > atf::kDecScratchCounterBytes / 4 || partial > atf::kDecScratchBytes - atf::kDecScratchCounterBytes)
+    return fail(ATF_ERR_UNSUPPORTED,
+                "decode without allocation: %zu sequence x kv head pairs need %zu bytes of split partials; the fixed "
+                "scratch holds %zu pairs and %zu bytes (use atf_decode_paged_bf16 with a workspace)",
+                pairs, partial, atf::kDecScratchCounterBytes / 4,
+                atf::kDecScratchBytes - atf::kDecScratchCounterBytes);
+  hipError_t e = atf::launch_decode_noalloc(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "decode (no allocation) launch");
   return ok();
 }
 

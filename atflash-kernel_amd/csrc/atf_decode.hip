@@ -20,6 +20,8 @@
 // for a (sequence, kv head) -- it sees the device-scope arrival counter reach
 // n_splits - 1 -- merges the split partials by log-sum-exp, writes the output
 // and resets the counter to zero for the next call.
+#include <mutex>
+
 #include "atf_launch.h"
 
 namespace atf {
@@ -395,6 +397,58 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t s) {
   if (a.batch <= 0) return hipSuccess;
   hipLaunchKernelGGL(decode_kernel, dim3(a.n_splits, a.hkv, a.batch), dim3(kDecWaves * 64), 0, s, a);
   return hipGetLastError();
+}
+
+// ---- fixed scratch for the entry point that allocates nothing ----
+// One copy per GPU, held until the process ends.  In host code `scratch` is a
+// stand-in for the symbol, not a device address: kernels and copies take the
+// address hipGetSymbolAddress returns for the current device, kept per device.
+static __device__ __align__(256) uint8_t scratch[kDecScratchBytes];
+
+__global__ void zero_words_kernel(uint32_t* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t* g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device, null until set up
+
+// The current device's scratch; on its first use on a device, looks up the
+// symbol's address there and zeroes the arrival counters with a fill kernel
+// on `s` (every completed call leaves the counters it used at zero again).
+hipError_t device_scratch(hipStream_t s, uint8_t** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (p == nullptr) return hipErrorInvalidSymbol;
+    constexpr int n = static_cast<int>(kDecScratchCounterBytes / 4);
+    hipLaunchKernelGGL(zero_words_kernel, dim3((n + 255) / 256), dim3(256), 0, s, static_cast<uint32_t*>(p), n);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    g_scratch_ptr[dev] = static_cast<uint8_t*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return hipSuccess;
+}
+}  // namespace
+
+hipError_t launch_decode_noalloc(DecodeArgs a, hipStream_t s) {
+  if (a.batch <= 0) return hipSuccess;
+  uint8_t* base = nullptr;
+  hipError_t e = device_scratch(s, &base);
+  if (e != hipSuccess) return e;
+  a.counters = reinterpret_cast<uint32_t*>(base);
+  a.ws_ml = reinterpret_cast<float*>(base + kDecScratchCounterBytes);
+  a.ws_o = a.ws_ml + static_cast<size_t>(a.batch) * a.hkv * a.n_splits * kDecMaxGroup * 2;
+  return launch_decode(a, s);
 }
 
 hipError_t launch_decode_page_levels(int32_t* out, int n_pages, int seq_len, const LevelTable& lt,

@@ -146,6 +146,31 @@ int atf_decode_paged_bf16(void* out, int64_t o_sb, int64_t o_sh,
                           int layout, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * atf_decode_paged_bf16 for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  It has no counterpart in the reference.  Same arguments and
+ * result as atf_decode_paged_bf16 without the workspace: the split partials and
+ * arrival counters live in a fixed 8 MiB scratch array in device memory, one
+ * per GPU the library runs on, held until the process ends.  No call allocates
+ * or frees anything.  Limits: at most 4096 (sequence, kv head) pairs and
+ * batch * num_kv_heads * splits * 16 * 130 * 4 bytes of partials within
+ * 8 MiB - 16 KiB (the split count is atf_decode_workspace_bytes' one; e.g.
+ * B * Hkv <= 1006 for short contexts); larger requests return
+ * ATF_ERR_UNSUPPORTED.  The first call on a device looks up the array's
+ * address there and zeroes its counters with a kernel on `stream`; the current
+ * device must be the stream's.  Every call on a GPU shares that GPU's scratch
+ * and leaves its counters at zero: calls that overlap on one GPU (different
+ * streams, other threads) race.
+ */
+int atf_decode_paged_bf16_noalloc(void* out, int64_t o_sb, int64_t o_sh,
+                                  const void* q, int64_t q_sb, int64_t q_sh,
+                                  const void* k_cache, const void* v_cache, int num_pages,
+                                  const int32_t* page_table, int max_pages, const int32_t* seq_lens,
+                                  int batch, int num_q_heads, int num_kv_heads, int max_seq_len,
+                                  const int32_t* zhi, float sm_scale, const float* rope_cs, int rope_max_pos,
+                                  int layout, void* stream);
+
+/*
  * Per-tile level counts (D_eff / 16) as the kernels compute them, for tests of
  * the integer window path.  prefill: out int32 [n_row_tiles][n_kblocks] for
  * 32-row query tiles starting at q_offset + 32*i and 32-key blocks;

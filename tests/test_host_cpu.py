@@ -189,6 +189,23 @@ def test_validation_status_codes():
     assert L.atf_decode_page_levels(None, 4, 64, None, None) == INV
 
 
+def test_noalloc_decode_refuses_oversize_requests():
+    """The decode entry point without a workspace refuses requests its fixed
+    scratch cannot hold (here 8192 sequences x 1 kv head > 4096 counters) before
+    any device work (the pointers are never used)."""
+    _lib = _lib_or_skip()
+    L = _lib.lib()
+    a = dict(out=FAKE, o_sb=0, o_sh=0, q=FAKE, q_sb=0, q_sh=0, k=FAKE, v=FAKE, num_pages=8, table=FAKE,
+             max_pages=8, seq_lens=FAKE, batch=8192, hq=4, hkv=1, max_seq_len=128, zhi=None, scale=0.088,
+             rope=None, rope_max=0, layout=0, stream=None)
+    assert L.atf_decode_paged_bf16_noalloc(*a.values()) == _lib.ATF_ERR_UNSUPPORTED
+    assert b"scratch" in L.atf_last_error()
+    a.update(batch=1, hq=68, hkv=4)
+    assert L.atf_decode_paged_bf16_noalloc(*a.values()) == _lib.ATF_ERR_UNSUPPORTED   # GQA group 17
+    a.update(batch=-1, hq=4, hkv=1)
+    assert L.atf_decode_paged_bf16_noalloc(*a.values()) == _lib.ATF_ERR_INVALID
+
+
 def test_table_cap_below_longest_distance_is_refused():
     """zhi[0] is the table's cap; a cap below the call's longest causal distance
     would drop levels the rule keeps (e2e_pipeline/atflash_e2e_fafi.py:55-58), so

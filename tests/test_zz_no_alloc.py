@@ -1,0 +1,68 @@
+"""The decode entry point that allocates nothing (atf_decode_paged_bf16_noalloc),
+called through the C ABI and checked against atf_decode_paged_bf16 with a
+workspace (same kernel, same split count: equal bit for bit) on consecutive
+calls, the second smaller than the first, and the first again afterwards (the
+shared scratch keeps the last call's contents; its counters must be back at
+zero).  Outputs are preallocated by the test; the entry point itself allocates
+nothing."""
+import pytest
+import torch
+
+import helpers as H
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(lens, hq, hkv, base, k_ret, rope, dev, seed):
+    from atflash import atflash_window as AW, ops, rope as R  # noqa: F401  (ops registers torch.ops.atflash)
+    from atflash.cache import PagedKVCache
+    cache = PagedKVCache(sum(-(-n // 16) for n in lens) + 5, hkv, dev)
+    cache._free = torch.randperm(cache.num_pages, generator=torch.Generator().manual_seed(seed)).tolist()
+    rt = R.rope_table(max(lens), R.inv_freq(H.D, base, dev)) if rope else None
+    for b, n in enumerate(lens):
+        cache.add_sequence(b, n)
+    table = cache.page_table(list(range(len(lens))))
+    for b, n in enumerate(lens):
+        _, k, v = H.gpu_qkv(1, n, 1, hkv, dev, seed=seed + b, nq=1)
+        torch.ops.atflash.kv_write(cache.k, cache.v, k, v, torch.zeros(1, dtype=torch.int32, device=dev),
+                                   table[b:b + 1].contiguous(), rt, 0)
+    q = H.gpu_qkv(len(lens), 1, hq, 1, dev, seed=seed + 100, nq=1)[0][:, 0]  # [B, Hq, 128]
+    zhi = None if k_ret is None else AW.window_zhi_from_kret(H.D, base, k_ret, 1 << 23)
+    return dict(cache=cache, table=table, q=q, rt=rt, zhi=zhi, lens=lens, hq=hq, hkv=hkv,
+                seq=torch.tensor(lens, dtype=torch.int32, device=dev))
+
+
+def _decode(c, noalloc):
+    from atflash import _lib
+    L = _lib.lib()
+    B, maxlen = len(c["lens"]), max(c["lens"])
+    out = torch.empty((B, c["hq"], H.D), dtype=torch.bfloat16, device=c["q"].device)
+    rt = c["rt"]
+    args = [_lib.ptr(out), out.stride(0), out.stride(1), _lib.ptr(c["q"]), c["q"].stride(0), c["q"].stride(1),
+            _lib.ptr(c["cache"].k), _lib.ptr(c["cache"].v), c["cache"].num_pages, _lib.ptr(c["table"]),
+            c["table"].shape[1], _lib.ptr(c["seq"]), B, c["hq"], c["hkv"], maxlen, _lib.zhi_array(c["zhi"]),
+            H.D ** -0.5, _lib.ptr(rt), 0 if rt is None else rt.shape[0], 0]
+    if noalloc:
+        _lib.check(L.atf_decode_paged_bf16_noalloc(*args, _lib.stream_of(out.device)))
+    else:
+        nbytes = L.atf_decode_workspace_bytes(B, c["hq"], c["hkv"], maxlen)
+        ws = torch.zeros((nbytes + 3) // 4, dtype=torch.float32, device=out.device)
+        _lib.check(L.atf_decode_paged_bf16(*args, _lib.ptr(ws), nbytes, _lib.stream_of(out.device)))
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+def test_noalloc_decode_equals_workspace_decode(dev):
+    print("[noalloc] call 1: B=3 Qwen shape, 20000/9000/777 tokens, k=2, RoPE at load", flush=True)
+    big = _case([20000, 9000, 777], 28, 4, 1e7, 2.0, True, dev, seed=71)
+    print("[noalloc] call 2: B=1 Llama shape, 3000 tokens, window OFF, pre-rotated", flush=True)
+    small = _case([3000], 24, 8, 5e5, None, False, dev, seed=72)
+    a = _decode(big, noalloc=True)
+    assert torch.equal(a, _decode(big, noalloc=False))
+    s = _decode(small, noalloc=True)
+    assert torch.equal(s, _decode(small, noalloc=False))
+    assert torch.equal(_decode(big, noalloc=True), a)
+    # and against the fp32 oracle for the short sequence of the first call
+    k, v = [t.cpu() for t in H.gpu_qkv(1, 777, 1, 4, dev, seed=71 + 2, nq=1)[1:]]
+    ref = H.decode_oracle(big["q"][2].cpu(), k[0], v[0], 1e7, 2.0, True)
+    H.assert_close(a[2], ref, "noalloc, 777 tokens")
