@@ -46,7 +46,6 @@ SIGNATURES = {
     "atf_prefill_bf16": (_i, [_p, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _p, _i, _p, _i,
                               _i, _i, _i, _i, _i, _i, _p, _f, _p, _i, _i, _p]),
     "atf_decode_workspace_bytes": (_sz, [_i, _i, _i, _i]),
-    "atf_decode_counter_bytes": (_sz, [_i, _i]),
     "atf_decode_paged_bf16": (_i, [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i, _p, _i, _p,
                                    _i, _i, _i, _i, _p, _f, _p, _i, _i, _p, _sz, _p]),
     "atf_decode_paged_bf16_noalloc": (_i, [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i, _p, _i, _p,

@@ -115,27 +115,19 @@ def _(q, k_cache, v_cache, page_table, nk, q_offset, zhi, sm_scale, rope_cs, lay
     return q.new_empty((B, Nq, Hq, D)), q.new_empty((B, Hq, Nq), dtype=torch.float32)
 
 
-# Decode workspaces, one per (device, stream), each with the number of leading
-# bytes known to be zero.  A call needs its arrival-counter region (the first
-# atf_decode_counter_bytes(B, Hkv) bytes) zero when it starts and leaves exactly
-# that region zero when it completes; the bytes after it then hold split
-# partials.  A call whose counter region is larger than the known-zero prefix
-# (more sequences x kv heads than the previous call) zeroes its region first,
-# with a fill kernel on the call's stream.  Calls on one stream are ordered, so
-# they can share a workspace.
+# Decode workspaces, one per (device, stream), grown on demand.  A workspace
+# needs no initialisation (each call writes the split partials it reads), and
+# calls on one stream are ordered, so they can share it.
 _DECODE_WS = {}
 
 
-def _decode_workspace(device, nbytes, counter_bytes):
+def _decode_workspace(device, nbytes):
     stream = torch.cuda.current_stream(device)
     key = (device.index, stream.cuda_stream)
-    ws, zero = _DECODE_WS.get(key, (None, 0))
+    ws = _DECODE_WS.get(key)
     if ws is None or ws.numel() * 4 < nbytes:
-        ws = torch.zeros((max(nbytes, 16) + 3) // 4, dtype=torch.float32, device=device)
-        zero = ws.numel() * 4
-    elif zero < counter_bytes:
-        ws[: counter_bytes // 4].zero_()
-    _DECODE_WS[key] = (ws, counter_bytes)
+        ws = torch.empty((max(nbytes, 16) + 3) // 4, dtype=torch.float32, device=device)
+        _DECODE_WS[key] = ws
     return ws
 
 
@@ -158,7 +150,7 @@ def decode_paged(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
     rope_cs, max_pos = _rope(rope_cs)
     L = _lib.lib()
     nbytes = int(L.atf_decode_workspace_bytes(B, Hq, hkv, int(max_seq_len)))
-    ws = _decode_workspace(q.device, nbytes, int(L.atf_decode_counter_bytes(B, hkv)))
+    ws = _decode_workspace(q.device, nbytes)
     out = torch.empty((B, Hq, _lib.HEAD_DIM), dtype=torch.bfloat16, device=q.device)
     _lib.check(L.atf_decode_paged_bf16(
         _lib.ptr(out), out.stride(0), out.stride(1), _lib.ptr(q), q.stride(0), q.stride(1),

@@ -85,10 +85,10 @@ void decode_split(int batch, int hkv, int max_seq_len, int* n_splits, int* pages
   *n_splits = (pages + pps - 1) / pps;
 }
 
-// Workspace: [counters: B*Hkv uint32, padded to kDecCounterBytes][ws_ml][ws_o].
-size_t counter_bytes(int batch, int hkv) {
-  const size_t c = static_cast<size_t>(batch) * hkv * sizeof(uint32_t);
-  return (c + atf::kDecCounterBytes - 1) / atf::kDecCounterBytes * atf::kDecCounterBytes;
+// Bytes of split partials ([ws_ml][ws_o], fp32): none with one split.
+size_t partial_bytes(int batch, int hkv, int ns) {
+  if (ns <= 1) return 0;
+  return static_cast<size_t>(batch) * hkv * ns * atf::kDecMaxGroup * (atf::kD + 2) * sizeof(float);
 }
 
 }  // namespace
@@ -197,13 +197,7 @@ size_t atf_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, 
   if (batch <= 0 || num_kv_heads <= 0) return 0;
   int ns = 1, pps = 1;
   decode_split(batch, num_kv_heads, max_seq_len, &ns, &pps);
-  return counter_bytes(batch, num_kv_heads) +
-         static_cast<size_t>(batch) * num_kv_heads * ns * atf::kDecMaxGroup * (atf::kD + 2) * sizeof(float);
-}
-
-size_t atf_decode_counter_bytes(int batch, int num_kv_heads) {
-  if (batch <= 0 || num_kv_heads <= 0) return 0;
-  return counter_bytes(batch, num_kv_heads);
+  return partial_bytes(batch, num_kv_heads, ns);
 }
 
 }  // extern "C"
@@ -279,14 +273,13 @@ int atf_decode_paged_bf16(void* out, int64_t o_sb, int64_t o_sh, const void* q, 
                              seq_lens, batch, num_q_heads, num_kv_heads, max_seq_len, zhi, sm_scale, rope_cs,
                              rope_max_pos, layout, &a))
     return r;
-  const size_t need = atf_decode_workspace_bytes(batch, num_q_heads, num_kv_heads, max_seq_len);
-  if (!workspace || workspace_bytes < need || !aligned(workspace, 16))
+  const size_t need = partial_bytes(batch, num_kv_heads, a.n_splits);
+  if (need > 0 && (!workspace || workspace_bytes < need || !aligned(workspace, 16)))
     return fail(ATF_ERR_WORKSPACE, "workspace of %zu bytes (16-byte aligned) required, got %zu", need,
                 workspace ? workspace_bytes : 0);
-  char* ws = static_cast<char*>(workspace);
-  a.counters = reinterpret_cast<uint32_t*>(ws);
-  a.ws_ml = reinterpret_cast<float*>(ws + counter_bytes(batch, num_kv_heads));
-  a.ws_o = a.ws_ml + static_cast<size_t>(batch) * num_kv_heads * a.n_splits * atf::kDecMaxGroup * 2;
+  a.ws_ml = static_cast<float*>(workspace);
+  a.ws_o = need > 0 ? a.ws_ml + static_cast<size_t>(batch) * num_kv_heads * a.n_splits * atf::kDecMaxGroup * 2
+                    : nullptr;
   hipError_t e = atf::launch_decode(a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "decode launch");
   return ok();
@@ -304,14 +297,12 @@ int atf_decode_paged_bf16_noalloc(void* out, int64_t o_sb, int64_t o_sh, const v
                              seq_lens, batch, num_q_heads, num_kv_heads, max_seq_len, zhi, sm_scale, rope_cs,
                              rope_max_pos, layout, &a))
     return r;
-  const size_t pairs = static_cast<size_t>(batch) * num_kv_heads;
-  const size_t partial = pairs * a.n_splits * atf::kDecMaxGroup * (atf::kD + 2) * sizeof(float);
-  if (pairs > atf::kDecScratchCounterBytes / 4 || partial > atf::kDecScratchBytes - atf::kDecScratchCounterBytes)
+  const size_t partial = partial_bytes(batch, num_kv_heads, a.n_splits);
+  if (partial > atf::kDecScratchBytes)
     return fail(ATF_ERR_UNSUPPORTED,
-                "decode without allocation: %zu sequence x kv head pairs need %zu bytes of split partials; the fixed "
-                "scratch holds %zu pairs and %zu bytes (use atf_decode_paged_bf16 with a workspace)",
-                pairs, partial, atf::kDecScratchCounterBytes / 4,
-                atf::kDecScratchBytes - atf::kDecScratchCounterBytes);
+                "decode without allocation: %d x %d sequence x kv head pairs need %zu bytes of split partials; the "
+                "fixed scratch holds %zu (use atf_decode_paged_bf16 with a workspace)",
+                batch, num_kv_heads, partial, atf::kDecScratchBytes);
   hipError_t e = atf::launch_decode_noalloc(a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "decode (no allocation) launch");
   return ok();

@@ -15,21 +15,21 @@
 // loads of the other levels are never issued, so out-of-window K bytes are not
 // read from HBM.
 //
-// Merging, all in the one launch: the 8 wave partials (m, l, o) of a split are
-// combined in LDS and written to the workspace; the last workgroup to finish
-// for a (sequence, kv head) -- it sees the device-scope arrival counter reach
-// n_splits - 1 -- merges the split partials by log-sum-exp, writes the output
-// and resets the counter to zero for the next call.
+// Merging: the 8 wave partials (m, l, o) of a split are combined in LDS.  With
+// one split per (sequence, kv head) the workgroup writes the output itself.
+// Otherwise it stores the split's partial in the workspace and ends, and a
+// second kernel (decode_merge_kernel, one workgroup per (sequence, kv head))
+// merges the split partials by log-sum-exp and writes the output.  The kernel
+// boundary orders the partial stores before the merge loads, so no workgroup
+// waits on another inside a launch: no arrival counters, atomics or fences.
+// (Measured against merging in the last-arriving workgroup of one launch: the
+// chain store -> wait -> arrival atomic -> acquire -> loads there kept a single
+// workgroup busy for about 7 us after the last split finished.)
 #include <mutex>
 
 #include "atf_launch.h"
 
 namespace atf {
-
-// s_waitcnt immediate for vmcnt(0) alone (gfx9 encoding: vmcnt bits 3:0 and
-// 15:14, expcnt 6:4, lgkmcnt 11:8), issued through the builtin so the
-// compiler's own wait insertion accounts for it.
-constexpr int kWaitVm = 0x0F70;
 
 // Word 3 of a raw buffer resource (no format conversion, 32-bit data format
 // field), as the raw buffer-load path of gfx9-family targets expects.
@@ -112,13 +112,9 @@ __device__ __forceinline__ void dec_load_page(const DecodeArgs& a, int h, int ra
 // two waves per SIMD: at most 256 registers per wave
 __global__ __launch_bounds__(kDecWaves * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void decode_kernel(DecodeArgs a) {
-  // wave partials; in the merging workgroup, afterwards, the partial merges of
-  // up to 8 threads per (query head, dims) (o in sh_o, m and l in red)
+  // wave partials
   __shared__ __attribute__((aligned(16))) float sh_o[kDecWaves * kDecMaxGroup * kD];
   __shared__ float sh_m[kDecWaves * kDecMaxGroup], sh_l[kDecWaves * kDecMaxGroup];
-  __shared__ float red[kDecWaves * 64];
-  __shared__ int sh_last;
-  static_assert(kDecWaves >= 8 && kDecWaves * 64 >= 2 * 8 * kDecMaxGroup, "merge staging must fit sh_o and red");
 
   const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x;
@@ -281,48 +277,49 @@ void decode_kernel(DecodeArgs a) {
         acc += wt * *reinterpret_cast<const f32x4*>(&sh_o[(w * kDecMaxGroup + gq) * kD + d4]);
       }
     }
-    // Agent-scope stores: written through to the device coherence point, so no
-    // L2 write-back is needed before the arrival count below.
-    const int64_t pi = pbase + static_cast<int64_t>(s) * kDecMaxGroup + gq;
-    float* po = a.ws_o + pi * kD + d4;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) __hip_atomic_store(po + i, acc[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (d4 == 0) {
-      __hip_atomic_store(a.ws_ml + pi * 2 + 0, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(a.ws_ml + pi * 2 + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (a.n_splits == 1) {  // the split is the whole sequence: write the output
+      const float inv = L > 0.f ? 1.f / L : 0.f;
+      uint16_t* out = a.out + static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(h * a.group + gq) * a.o_sh + d4;
+      u32x2 pk;
+      pk[0] = pack_bf16x2(acc[0] * inv, acc[1] * inv);
+      pk[1] = pack_bf16x2(acc[2] * inv, acc[3] * inv);
+      *reinterpret_cast<u32x2*>(out) = pk;
+    } else {  // the split's partial, merged by decode_merge_kernel
+      const int64_t pi = pbase + static_cast<int64_t>(s) * kDecMaxGroup + gq;
+      *reinterpret_cast<f32x4*>(a.ws_o + pi * kD + d4) = acc;
+      if (d4 == 0) *reinterpret_cast<f32x2*>(a.ws_ml + pi * 2) = f32x2{M, L};
     }
   }
+}
 
-  // ---- arrival: the last split of (b, h) to finish merges all splits ----
-  // The partials were stored at agent scope, and the barrier waits until every
-  // wave's stores have completed there, so thread 0's increment needs no
-  // release fence: a device-scope release writes back the whole XCD L2, and
-  // with 32 workgroups per XCD finishing together those write-backs serialize.
-  // (The workgroup barrier alone does not wait for stores: vmcnt(0) is explicit.)
-  __builtin_amdgcn_s_waitcnt(kWaitVm);
-  __syncthreads();
-  uint32_t* cnt = a.counters + (static_cast<int64_t>(b) * a.hkv + h);
-  if (tid == 0) {
-    const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int last = (old == static_cast<uint32_t>(a.n_splits - 1)) ? 1 : 0;
-    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // the other splits' partials are visible
-    sh_last = last;
-  }
-  __syncthreads();
-  if (!sh_last) return;
+// Log-sum-exp merge of the split partials, launched after decode_kernel when
+// n_splits > 1.  One workgroup per (dim chunk of 32, kv head, sequence), so
+// that the merge's loads spread over 4 CUs per (sequence, kv head): a single
+// workgroup per (sequence, kv head) issued 4x as many loads from one CU and
+// took about as long as the tail it replaced.  Thread t takes dims
+// 32 * chunk + 4 * (t % 8) .. +3 of query head mg and every H-th split
+// starting at hh (H as large as G * H <= 64 allows, so the split loop is
+// short).  It loads the (m, l) and o of up to kBatch splits before using any
+// of them, so with up to 32 splits per thread the merge costs one memory round
+// trip; more splits are folded in batch by batch with a running max.  The H
+// partial merges of a (head, dims) are combined through LDS.
+constexpr int kMergeChunks = 4;
+constexpr int kMergeDims = kD / kMergeChunks;  // 32
 
-  // ---- merge of the split partials (the last workgroup of (b, h) only) ----
-  // Thread t takes query head gq, dims d4..d4+3 and every H-th split starting at
-  // hh, with H threads per (head, dims) so that all 512 threads load.  It loads
-  // the (m, l) and o of up to kBatch splits before using any of them, so with up
-  // to 32 splits per thread the merge costs one memory round trip; more splits
-  // are folded in batch by batch with a running max.  The H partial merges of a
-  // (head, dims) are then combined through LDS.
+__global__ __launch_bounds__(kDecWaves * 64) void decode_merge_kernel(DecodeArgs a) {
+  __shared__ __attribute__((aligned(16))) float sh_o[64 * kMergeDims];
+  __shared__ float red[2 * 64];
+  const int chunk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const float NEG_INF = -__builtin_huge_valf();
+  const float c = a.scale_log2;
+  const int64_t pbase = (static_cast<int64_t>(b) * a.hkv + h) * a.n_splits * kDecMaxGroup;  // split 0, head 0
   constexpr int kBatch = 32;
-  const int H = (a.group <= 2) ? 8 : (a.group <= 4) ? 4 : (a.group <= 8) ? 2 : 1;
-  const int mr = tid >> 5;  // 0..15
-  const int mg = mr / H, hh = mr - (mr / H) * H;
-  const int md4 = 4 * (tid & 31);
+  const int H = (a.group <= 1) ? 64 : (a.group <= 2) ? 32 : (a.group <= 4) ? 16 : (a.group <= 8) ? 8 : 4;
+  const int row = tid >> 3;  // 0..63: (head, split group)
+  const int mg = row / H, hh = row - (row / H) * H;
+  const int q4 = 4 * (tid & 7);
+  const int md4 = chunk * kMergeDims + q4;
   const bool mact = mg < a.group;
   float m_t = NEG_INF, L_t = 0.f;
   f32x4 acc_t = f32x4{};
@@ -357,23 +354,23 @@ void decode_kernel(DecodeArgs a) {
         m_t = mb;
       }
     }
-    *reinterpret_cast<f32x4*>(&sh_o[(hh * kDecMaxGroup + mg) * kD + md4]) = acc_t;
-    if (md4 == 0) {
-      red[hh * kDecMaxGroup + mg] = m_t;
-      red[8 * kDecMaxGroup + hh * kDecMaxGroup + mg] = L_t;
+    *reinterpret_cast<f32x4*>(&sh_o[row * kMergeDims + q4]) = acc_t;
+    if (q4 == 0) {
+      red[row] = m_t;
+      red[64 + row] = L_t;
     }
   }
   __syncthreads();
   if (mact && hh == 0) {
     float M = NEG_INF;
-    for (int h2 = 0; h2 < H; ++h2) M = fmaxf(M, red[h2 * kDecMaxGroup + mg]);
+    for (int h2 = 0; h2 < H; ++h2) M = fmaxf(M, red[row + h2]);
     float L = 0.f;
     f32x4 o = f32x4{};
     if (M != NEG_INF) {
       for (int h2 = 0; h2 < H; ++h2) {
-        const float wt = fast_exp2((red[h2 * kDecMaxGroup + mg] - M) * c);
-        L += wt * red[8 * kDecMaxGroup + h2 * kDecMaxGroup + mg];
-        o += wt * *reinterpret_cast<const f32x4*>(&sh_o[(h2 * kDecMaxGroup + mg) * kD + md4]);
+        const float wt = fast_exp2((red[row + h2] - M) * c);
+        L += wt * red[64 + row + h2];
+        o += wt * *reinterpret_cast<const f32x4*>(&sh_o[(row + h2) * kMergeDims + q4]);
       }
     }
     const float inv = L > 0.f ? 1.f / L : 0.f;
@@ -383,7 +380,6 @@ void decode_kernel(DecodeArgs a) {
     pk[1] = pack_bf16x2(o[2] * inv, o[3] * inv);
     *reinterpret_cast<u32x2*>(out) = pk;
   }
-  if (tid == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Level count per page for one sequence of length N (decode rule, block_n = 16).
@@ -396,6 +392,9 @@ __global__ void decode_page_levels_kernel(int32_t* out, int n_pages, int N, Leve
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t s) {
   if (a.batch <= 0) return hipSuccess;
   hipLaunchKernelGGL(decode_kernel, dim3(a.n_splits, a.hkv, a.batch), dim3(kDecWaves * 64), 0, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || a.n_splits == 1) return e;
+  hipLaunchKernelGGL(decode_merge_kernel, dim3(kMergeChunks, a.hkv, a.batch), dim3(kDecWaves * 64), 0, s, a);
   return hipGetLastError();
 }
 
@@ -403,22 +402,16 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t s) {
 // One copy per GPU, held until the process ends.  In host code `scratch` is a
 // stand-in for the symbol, not a device address: kernels and copies take the
 // address hipGetSymbolAddress returns for the current device, kept per device.
+// It holds split partials only; nothing in it has to start at any value.
 static __device__ __align__(256) uint8_t scratch[kDecScratchBytes];
-
-__global__ void zero_words_kernel(uint32_t* p, int n) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0u;
-}
 
 namespace {
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
-uint8_t* g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device, null until set up
+uint8_t* g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device, null until looked up
 
-// The current device's scratch; on its first use on a device, looks up the
-// symbol's address there and zeroes the arrival counters with a fill kernel
-// on `s` (every completed call leaves the counters it used at zero again).
-hipError_t device_scratch(hipStream_t s, uint8_t** out) {
+// The current device's scratch, looked up on its first use on that device.
+hipError_t device_scratch(uint8_t** out) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
@@ -429,10 +422,6 @@ hipError_t device_scratch(hipStream_t s, uint8_t** out) {
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess) return e;
     if (p == nullptr) return hipErrorInvalidSymbol;
-    constexpr int n = static_cast<int>(kDecScratchCounterBytes / 4);
-    hipLaunchKernelGGL(zero_words_kernel, dim3((n + 255) / 256), dim3(256), 0, s, static_cast<uint32_t*>(p), n);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
     g_scratch_ptr[dev] = static_cast<uint8_t*>(p);
   }
   *out = g_scratch_ptr[dev];
@@ -443,10 +432,9 @@ hipError_t device_scratch(hipStream_t s, uint8_t** out) {
 hipError_t launch_decode_noalloc(DecodeArgs a, hipStream_t s) {
   if (a.batch <= 0) return hipSuccess;
   uint8_t* base = nullptr;
-  hipError_t e = device_scratch(s, &base);
+  hipError_t e = device_scratch(&base);
   if (e != hipSuccess) return e;
-  a.counters = reinterpret_cast<uint32_t*>(base);
-  a.ws_ml = reinterpret_cast<float*>(base + kDecScratchCounterBytes);
+  a.ws_ml = reinterpret_cast<float*>(base);
   a.ws_o = a.ws_ml + static_cast<size_t>(a.batch) * a.hkv * a.n_splits * kDecMaxGroup * 2;
   return launch_decode(a, s);
 }

@@ -19,13 +19,9 @@ constexpr int kDecMaxGroup = 16;
 constexpr int kDecUnroll = 4;      // pages in flight per wave
 constexpr int kDecWaves = 8;       // waves per workgroup (one split), 2 per SIMD
 constexpr int kDecMaxSplits = 256;
-constexpr int kDecCounterBytes = 256;  // counter region granularity in the workspace
 // Fixed device scratch of the entry point that allocates nothing
-// (atf_decode_paged_bf16_noalloc): arrival counters for up to
-// kDecScratchCounterBytes / 4 (sequence, kv head) pairs at its start, split
-// partials after them.
+// (atf_decode_paged_bf16_noalloc): split partials, laid out as in a workspace.
 constexpr size_t kDecScratchBytes = size_t(8) << 20;
-constexpr size_t kDecScratchCounterBytes = 16384;
 
 struct KvWriteArgs {
   uint16_t* k_cache;
@@ -81,8 +77,7 @@ struct DecodeArgs {
   const float* rope_cs;
   int layout;
   LevelTable lt;
-  uint32_t* counters;  // [B][Hkv], zero between calls
-  float* ws_ml;        // [B][Hkv][n_splits][16][2]
+  float* ws_ml;        // [B][Hkv][n_splits][16][2]   split partials (n_splits > 1)
   float* ws_o;         // [B][Hkv][n_splits][16][128]
 };
 
@@ -92,7 +87,7 @@ hipError_t launch_prefill_tile_levels(int32_t* out, int n_row_tiles, int n_kbloc
                                       const LevelTable& lt, hipStream_t s);
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t s);
 // launch_decode with the workspace pointers taken from the device's fixed
-// scratch (a.counters, a.ws_ml and a.ws_o are set here).
+// scratch (a.ws_ml and a.ws_o are set here).
 hipError_t launch_decode_noalloc(DecodeArgs a, hipStream_t s);
 hipError_t launch_decode_page_levels(int32_t* out, int n_pages, int seq_len, const LevelTable& lt,
                                      hipStream_t s);

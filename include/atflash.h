@@ -109,25 +109,19 @@ int atf_prefill_bf16(void* out, int64_t o_sb, int64_t o_st, int64_t o_sh, float*
                      int layout, void* stream);
 
 /*
- * Bytes of device workspace atf_decode_paged_bf16 needs for these sizes: an
- * arrival-counter region (one uint32 per (sequence, kv head), padded to 256 B)
- * at the start of the workspace, followed by the split partials.
- *
- * Zero rule: the first atf_decode_counter_bytes(batch, num_kv_heads) bytes of
- * the workspace must be zero when a call starts.  A completed call leaves
- * exactly that many leading bytes at zero; the bytes after them hold split
- * partials.  So a workspace zero-filled once serves any later call whose
- * counter region is no larger than the previous call's; before a call with a
- * larger batch * num_kv_heads, zero its counter region again (a call only
- * writes partials past its own counter region).  Calls that share a workspace
- * must be ordered on one stream (concurrent calls on one workspace race).
+ * Bytes of device workspace atf_decode_paged_bf16 needs for these sizes: the
+ * fp32 split partials (m, l, o) of every (sequence, kv head, split), 0 when the
+ * call runs one split per (sequence, kv head).  The workspace needs no
+ * initialisation: each call writes the partials it reads back.  Calls that
+ * share a workspace must be ordered on one stream (concurrent calls race).
  */
 size_t atf_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int max_seq_len);
-size_t atf_decode_counter_bytes(int batch, int num_kv_heads);
 
 /*
  * Windowed split-KV decode: one query token per sequence at position
- * seq_lens[b] - 1 attending to keys 0..seq_lens[b]-1 of the paged cache.
+ * seq_lens[b] - 1 attending to keys 0..seq_lens[b]-1 of the paged cache.  It
+ * enqueues one kernel, plus a second that merges the split partials when a
+ * sequence is split (long contexts, small batches).
  * q/out are bf16 [batch][num_q_heads][128] with element strides (q: 16-byte
  * aligned, strides multiples of 8; out: 8-byte aligned, strides multiples of 4); seq_lens is a
  * device int32 [batch] whose entries must not exceed max_seq_len.  The window
@@ -149,18 +143,15 @@ int atf_decode_paged_bf16(void* out, int64_t o_sb, int64_t o_sh,
  * atf_decode_paged_bf16 for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  It has no counterpart in the reference.  Same arguments and
- * result as atf_decode_paged_bf16 without the workspace: the split partials and
- * arrival counters live in a fixed 8 MiB scratch array in device memory, one
- * per GPU the library runs on, held until the process ends.  No call allocates
- * or frees anything.  Limits: at most 4096 (sequence, kv head) pairs and
- * batch * num_kv_heads * splits * 16 * 130 * 4 bytes of partials within
- * 8 MiB - 16 KiB (the split count is atf_decode_workspace_bytes' one; e.g.
- * B * Hkv <= 1006 for short contexts); larger requests return
- * ATF_ERR_UNSUPPORTED.  The first call on a device looks up the array's
- * address there and zeroes its counters with a kernel on `stream`; the current
- * device must be the stream's.  Every call on a GPU shares that GPU's scratch
- * and leaves its counters at zero: calls that overlap on one GPU (different
- * streams, other threads) race.
+ * result as atf_decode_paged_bf16 without the workspace: the split partials
+ * live in a fixed 8 MiB scratch array in device memory, one per GPU the library
+ * runs on, held until the process ends.  No call allocates or frees anything.
+ * Limit: atf_decode_workspace_bytes(...) <= 8 MiB, otherwise
+ * ATF_ERR_UNSUPPORTED; the split rule keeps every request within about 4.1 MiB
+ * (fewer than 512 sequence x kv head x split triples).  The first call on a
+ * device looks up the array's address there; the current device must be the
+ * stream's.  Every call on a GPU shares that GPU's scratch: calls that overlap
+ * on one GPU (different streams, other threads) race.
  */
 int atf_decode_paged_bf16_noalloc(void* out, int64_t o_sb, int64_t o_sh,
                                   const void* q, int64_t q_sb, int64_t q_sh,

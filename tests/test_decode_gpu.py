@@ -133,8 +133,8 @@ def test_hnd_layout_and_strided_q(dev):
 
 
 def test_workspace_reuse_across_calls(dev):
-    """The cached workspace's arrival counters return to zero after each call:
-    a large call, a smaller one, then the large one again (bitwise equal)."""
+    """The cached workspace serves calls of other sizes: a large call, a smaller
+    one, then the large one again (bitwise equal)."""
     from atflash import interface
     g = torch.Generator().manual_seed(21)
     big = [H.randn_bf16(s, g) for s in ((28, H.D), (6000, 4, H.D), (6000, 4, H.D))]
@@ -151,10 +151,9 @@ def test_workspace_reuse_across_calls(dev):
 
 
 def test_workspace_reuse_with_more_sequences_and_heads(dev):
-    """A call whose counter region (one uint32 per sequence x kv head) is larger
-    than the previous call's reuses the cached workspace: B = 1 x 4 kv heads at
-    20K tokens (256 B of counters, then partials), then B = 32 x 4 kv heads at
-    300 tokens (512 B of counters over the first call's partials), then the
+    """The cached workspace across calls with different sequence x kv-head
+    counts and split counts: B = 1 x 4 kv heads at 20K tokens (40 splits), then
+    B = 32 x 4 kv heads at 300 tokens (one split each, no partials), then the
     first again.  Every output is checked against the oracle."""
     from atflash import interface, ops
     from atflash.cache import PagedKVCache

@@ -132,14 +132,29 @@ def test_workspace_size_formula():
     L = _lib.lib()
     assert L.atf_decode_workspace_bytes(0, 28, 4, 131072) == 0
     n = L.atf_decode_workspace_bytes(1, 28, 4, 131072)
-    # counters (padded to 256 B) + per split 16 heads x (128 + 2) fp32
-    assert (n - 256) % (4 * 16 * 130 * 4) == 0
-    ns = (n - 256) // (4 * 16 * 130 * 4)
-    assert 1 <= ns <= 256
+    # per split 16 query-head slots x (128 + 2) fp32
+    assert n % (4 * 16 * 130 * 4) == 0
+    ns = n // (4 * 16 * 130 * 4)
+    assert 2 <= ns <= 256
+    assert L.atf_decode_workspace_bytes(1, 28, 4, 300) == 0        # one split: no partials
+    assert L.atf_decode_workspace_bytes(64, 28, 4, 131072) == 0    # 256 sequence x kv head pairs: one split each
+    # the split rule keeps every request's partials under 512 triples (the fixed scratch of the
+    # entry point without allocation is 8 MiB)
+    worst = max(L.atf_decode_workspace_bytes(b, 8, 1, 1 << 20) for b in range(1, 300))
+    assert worst < 512 * 16 * 130 * 4 <= 8 << 20
     assert L.atf_decode_workspace_bytes(8, 24, 8, 163840) >= L.atf_decode_workspace_bytes(1, 24, 8, 163840)
 
 
 FAKE = ctypes.c_void_p(0x10000)  # never dereferenced: every call below fails validation first
+
+
+@pytest.fixture
+def no_gpu():
+    """The fake-pointer calls below must stop at argument validation; so that a
+    change in validation can never turn one into a kernel launch on fake
+    pointers, they run only where no GPU is visible (the CPU tier)."""
+    if torch.cuda.is_available():
+        pytest.skip("fake-pointer validation tests run on the CPU tier only")
 
 
 def _prefill(L, **kw):
@@ -151,14 +166,16 @@ def _prefill(L, **kw):
 
 
 def _decode(L, **kw):
-    a = dict(out=FAKE, o_sb=0, o_sh=0, q=FAKE, q_sb=0, q_sh=0, k=FAKE, v=FAKE, num_pages=8, table=FAKE,
-             max_pages=8, seq_lens=FAKE, batch=1, hq=28, hkv=4, max_seq_len=128, zhi=None, scale=0.088,
+    # 4096 tokens: several splits, so a workspace is required and the calls below
+    # stop at validation (at the latest at the workspace check)
+    a = dict(out=FAKE, o_sb=0, o_sh=0, q=FAKE, q_sb=0, q_sh=0, k=FAKE, v=FAKE, num_pages=256, table=FAKE,
+             max_pages=256, seq_lens=FAKE, batch=1, hq=28, hkv=4, max_seq_len=4096, zhi=None, scale=0.088,
              rope=None, rope_max=0, layout=0, ws=FAKE, ws_bytes=0, stream=None)
     a.update(kw)
     return L.atf_decode_paged_bf16(*a.values())
 
 
-def test_validation_status_codes():
+def test_validation_status_codes(no_gpu):
     _lib = _lib_or_skip()
     L = _lib.lib()
     INV, UNS, WS = _lib.ATF_ERR_INVALID, _lib.ATF_ERR_UNSUPPORTED, _lib.ATF_ERR_WORKSPACE
@@ -189,24 +206,22 @@ def test_validation_status_codes():
     assert L.atf_decode_page_levels(None, 4, 64, None, None) == INV
 
 
-def test_noalloc_decode_refuses_oversize_requests():
-    """The decode entry point without a workspace refuses requests its fixed
-    scratch cannot hold (here 8192 sequences x 1 kv head > 4096 counters) before
-    any device work (the pointers are never used)."""
+def test_noalloc_decode_validates_like_the_workspace_entry_point(no_gpu):
+    """The decode entry point without a workspace runs the same argument checks
+    before any device work (the pointers are never used)."""
     _lib = _lib_or_skip()
     L = _lib.lib()
     a = dict(out=FAKE, o_sb=0, o_sh=0, q=FAKE, q_sb=0, q_sh=0, k=FAKE, v=FAKE, num_pages=8, table=FAKE,
-             max_pages=8, seq_lens=FAKE, batch=8192, hq=4, hkv=1, max_seq_len=128, zhi=None, scale=0.088,
+             max_pages=8, seq_lens=FAKE, batch=1, hq=4, hkv=1, max_seq_len=0, zhi=None, scale=0.088,
              rope=None, rope_max=0, layout=0, stream=None)
-    assert L.atf_decode_paged_bf16_noalloc(*a.values()) == _lib.ATF_ERR_UNSUPPORTED
-    assert b"scratch" in L.atf_last_error()
-    a.update(batch=1, hq=68, hkv=4)
+    assert L.atf_decode_paged_bf16_noalloc(*a.values()) == _lib.ATF_ERR_INVALID   # max_seq_len 0
+    a.update(max_seq_len=128, hq=68, hkv=4)
     assert L.atf_decode_paged_bf16_noalloc(*a.values()) == _lib.ATF_ERR_UNSUPPORTED   # GQA group 17
     a.update(batch=-1, hq=4, hkv=1)
     assert L.atf_decode_paged_bf16_noalloc(*a.values()) == _lib.ATF_ERR_INVALID
 
 
-def test_table_cap_below_longest_distance_is_refused():
+def test_table_cap_below_longest_distance_is_refused(no_gpu):
     """zhi[0] is the table's cap; a cap below the call's longest causal distance
     would drop levels the rule keeps (e2e_pipeline/atflash_e2e_fafi.py:55-58), so
     the boundary refuses it.  The calls below stop at that check (the pointers
@@ -219,26 +234,11 @@ def test_table_cap_below_longest_distance_is_refused():
     assert short[0] == 126
     assert _prefill(L, zhi=short) == INV
     assert b"cap" in L.atf_last_error()
-    ws = L.atf_decode_workspace_bytes(1, 28, 4, 128)
-    assert _decode(L, zhi=short, ws_bytes=ws) == INV                   # max_seq_len 128: longest 127
+    assert _decode(L, zhi=short, max_seq_len=128) == INV               # longest distance 127
     assert b"cap" in L.atf_last_error()
     inf_short = (ctypes.c_int32 * 8)(*([100] * 8))                     # k = inf capped at 100
-    assert _decode(L, zhi=inf_short, ws_bytes=ws, max_seq_len=102) == INV
+    assert _decode(L, zhi=inf_short, max_seq_len=102) == INV
 
-
-def test_counter_region_size():
-    """The arrival-counter region at the start of the decode workspace: one
-    uint32 per (sequence, kv head), padded to 256 bytes."""
-    _lib = _lib_or_skip()
-    L = _lib.lib()
-    assert L.atf_decode_counter_bytes(0, 4) == 0
-    assert L.atf_decode_counter_bytes(1, 4) == 256
-    assert L.atf_decode_counter_bytes(64, 1) == 256
-    assert L.atf_decode_counter_bytes(65, 1) == 512
-    assert L.atf_decode_counter_bytes(32, 8) == 1024
-    for b, hkv, n in [(1, 4, 131072), (32, 4, 300), (8, 8, 163840)]:
-        c = L.atf_decode_counter_bytes(b, hkv)
-        assert (L.atf_decode_workspace_bytes(b, 28, hkv, n) - c) % (16 * 130 * 4) == 0
 
 
 # ---------------------------------------------------------------- Python operators

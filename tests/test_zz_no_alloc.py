@@ -2,8 +2,8 @@
 called through the C ABI and checked against atf_decode_paged_bf16 with a
 workspace (same kernel, same split count: equal bit for bit) on consecutive
 calls, the second smaller than the first, and the first again afterwards (the
-shared scratch keeps the last call's contents; its counters must be back at
-zero).  Outputs are preallocated by the test; the entry point itself allocates
+shared scratch keeps the last call's partials, which no later call may depend
+on).  Outputs are preallocated by the test; the entry point itself allocates
 nothing."""
 import pytest
 import torch
