@@ -174,6 +174,135 @@ def bench_gpu(args):
     return res
 
 
+# The reference's published timings (RTX PRO 6000, sm_120) for the other
+# configurations: (window OFF, window ON k=2).  Prefill: stock FA4 -> FA4 window
+# port (microbench/ports_fig/b1_bench_A.json:278,505,1292,1393;
+# b1_bench_A_n128k.json:88,125; microbench/7b_prefill_mb.json:42-140).  Decode:
+# stock FlashInfer -> FlashInfer window port, single request, medians of
+# times_ms (microbench/ports_fig/fiwin_bench2_rtx_sm120.json,
+# fiwin_bench2_n128k.json).  Their OFF is a different (stock) kernel; the ratio
+# here is always against this build's own window-OFF run.
+REF_PUBLISHED = {
+    "llama_prefill_ms": {8192: (1.328, 1.163), 32768: (20.40, 16.76), 131072: (329.63, 254.78)},
+    "llama_decode_b1_us": {8192: (36.35, 34.18), 32768: (94.94, 77.79), 131072: (340.32, 264.45),
+                           163840: (421.06, 325.02)},
+    "qwen_prefill_ms": {32768: (24.32, 20.81), 131072: (392.10, 320.53), 262144: (1642.0, 1330.2),
+                        524288: (7509.4, 5263.0)},
+}
+
+
+def _ref_ratio(table, n):
+    off, on = REF_PUBLISHED[table][n]
+    return {"reference_off": off, "reference_on": on, "reference_ratio": off / on}
+
+
+def bench_detail(steps=3):
+    """The other published configurations, each window OFF and k = 2 with the
+    ON/OFF ratio beside the reference's: Llama-3.2-3B prefill (24/8 heads, base
+    5e5) at 8K/32K/128K; Llama decode at batch 1 and 8 over 8K-160K (paged,
+    permuted pages, pools of >= 1 GiB rotated); Qwen2.5-7B prefill of 512K
+    tokens in 8K query chunks against the growing cache (attention only, the
+    cache pre-filled)."""
+    import torch
+    from atflash import atflash_window as AW, interface, ops, rope as R
+    from atflash.cache import PagedKVCache
+    dev = torch.device("cuda:0")
+    out = {"llama_prefill": {}, "llama_decode": {}, "qwen_prefill_chunked": {}}
+
+    def med(fn, n):
+        for _ in range(2):
+            fn()
+        return statistics.median(_events_time(fn, n))
+
+    # ---- Llama-3.2-3B prefill (attention kernel on a pre-packed cache) ----
+    hq, hkv, base = 24, 8, 5e5
+    for N in (8192, 32768, 131072):
+        g = torch.Generator(device=dev).manual_seed(N)
+        q = torch.randn((1, N, hq, D), generator=g, device=dev).to(torch.bfloat16)
+        k = torch.randn((1, N, hkv, D), generator=g, device=dev).to(torch.bfloat16)
+        v = torch.randn((1, N, hkv, D), generator=g, device=dev).to(torch.bfloat16)
+        rt = R.rope_table(N, R.inv_freq(D, base, dev))
+        kc, vc, table = interface.pack_kv(k, v, rope=rt)
+        r = {}
+        for name, zhi in (("off", None), ("k2", list(AW.window_zhi_from_kret(D, base, 2.0, 1 << 23)))):
+            r[name + "_ms"] = med(lambda: ops.prefill(q, kc, vc, table, N, 0, zhi, D ** -0.5, rt, 0), steps)
+        r["on_over_off"] = r["off_ms"] / r["k2_ms"]
+        r.update(_ref_ratio("llama_prefill_ms", N))
+        out["llama_prefill"][N] = r
+        print(f"[bench detail] llama prefill {N}: off {r['off_ms']:.2f} ms k2 {r['k2_ms']:.2f} ms "
+              f"({r['on_over_off']:.3f}x; reference {r['reference_ratio']:.3f}x)", flush=True)
+        del q, k, v, kc, vc, table, rt
+        torch.cuda.empty_cache()
+
+    # ---- Llama-3.2-3B decode, batch 1 and 8 ----
+    for B in (1, 8):
+        for N in (8192, 32768, 131072, 163840):
+            pages = -(-N // 16)
+            copies = max(1, math.ceil((1 << 30) / (B * pages * hkv * 8192)))
+            rt = R.rope_table(N, R.inv_freq(D, base, dev))
+            pool = PagedKVCache(copies * B * pages, hkv, dev)
+            g = torch.Generator(device=dev).manual_seed(B * N)
+            k = torch.randn((1, N, hkv, D), generator=g, device=dev).to(torch.bfloat16)
+            v = torch.randn((1, N, hkv, D), generator=g, device=dev).to(torch.bfloat16)
+            perm = torch.randperm(copies * B * pages, generator=torch.Generator().manual_seed(N + B))
+            tables = []
+            for c in range(copies):
+                tab = perm[c * B * pages:(c + 1) * B * pages].view(B, pages).to(torch.int32).to(dev)
+                for b in range(B):
+                    torch.ops.atflash.kv_write(pool.k, pool.v, k, v, torch.zeros(1, dtype=torch.int32, device=dev),
+                                               tab[b:b + 1].contiguous(), rt, 0)
+                tables.append(tab)
+            del k, v
+            q = torch.randn((B, hq, D), generator=g, device=dev).to(torch.bfloat16)
+            seq = torch.full((B,), N, dtype=torch.int32, device=dev)
+            r = {"kv_pool_bytes": copies * B * pages * hkv * 8192}
+            for name, zhi in (("off", None), ("k2", list(AW.window_zhi_from_kret(D, base, 2.0, 1 << 23)))):
+                it = [0]
+
+                def fn():
+                    t = tables[it[0] % copies]
+                    it[0] += 1
+                    return ops.decode_paged(q, pool.k, pool.v, t, seq, N, zhi, D ** -0.5, rt, 0)
+                for _ in range(10):
+                    fn()
+                r[name + "_us"] = _events_time_batch(fn, 40 * steps) * 1e3
+            r["on_over_off"] = r["off_us"] / r["k2_us"]
+            if B == 1:
+                r.update(_ref_ratio("llama_decode_b1_us", N))
+            out["llama_decode"][f"b{B}_{N}"] = r
+            print(f"[bench detail] llama decode B={B} {N}: off {r['off_us']:.1f} us k2 {r['k2_us']:.1f} us "
+                  f"({r['on_over_off']:.3f}x" + (f"; reference {r['reference_ratio']:.3f}x)" if B == 1 else ")"),
+                  flush=True)
+            del pool, tables, q, rt
+            torch.cuda.empty_cache()
+
+    # ---- Qwen2.5-7B prefill of 512K tokens in 8K query chunks ----
+    N, C = 524288, 8192
+    g = torch.Generator(device=dev).manual_seed(512)
+    q = torch.randn((1, N, HQ, D), generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn((1, N, HKV, D), generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn((1, N, HKV, D), generator=g, device=dev).to(torch.bfloat16)
+    rt = R.rope_table(N, R.inv_freq(D, BASE, dev))
+    kc, vc, table = interface.pack_kv(k, v, rope=rt)
+    del k, v
+    r = {}
+    for name, zhi in (("off", None), ("k2", list(AW.window_zhi_from_kret(D, BASE, 2.0, 1 << 23)))):
+        def fn():
+            for c0 in range(0, N, C):
+                ops.prefill(q[:, c0:c0 + C], kc, vc, table, c0 + C, c0, zhi, D ** -0.5, rt, 0)
+        fn()
+        r[name + "_ms"] = statistics.median(_events_time(fn, 2))
+    r["on_over_off"] = r["off_ms"] / r["k2_ms"]
+    r.update(_ref_ratio("qwen_prefill_ms", N))
+    r["reference_note"] = "reference: single-shot FA4 (stock OFF degrades past 256K)"
+    out["qwen_prefill_chunked"][N] = r
+    print(f"[bench detail] qwen prefill 512K in 8K chunks: off {r['off_ms']:.0f} ms k2 {r['k2_ms']:.0f} ms "
+          f"({r['on_over_off']:.3f}x; reference {r['reference_ratio']:.3f}x)", flush=True)
+    del q, kc, vc, table, rt
+    torch.cuda.empty_cache()
+    return out
+
+
 def slice_ratios(N):
     from atflash import atflash_window as AW, fiwin_common as FW
     out = {}
@@ -260,6 +389,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--n", type=int, default=131072)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-detail", action="store_true", help="skip the other published configurations")
     ap.add_argument("--only", choices=("all", "prefill", "decode", "kv_write", "copy"), default="all",
                     help="run one workload (for profiler runs); 'copy' is a plain 1 GiB device copy "
                          "used to calibrate the FETCH_SIZE / WRITE_SIZE counters")
@@ -293,6 +423,7 @@ def main():
         return
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_wall
+    detail_cfgs = None if args.no_detail else bench_detail()
     sr = slice_ratios(N)
 
     flops_off = 2.0 * HQ * N * N * D
@@ -376,6 +507,8 @@ def main():
             "stats": res,
         },
     }
+    if detail_cfgs is not None:
+        line["detail"]["configs"] = detail_cfgs
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(N)
     print(json.dumps(line))
