@@ -69,7 +69,8 @@ __device__ __forceinline__ float pair_sum(float x) {
 // Level count of tile t for a fixed (query anchor, key offset) pair as t walks
 // up: level i is read from tile T_i = ceil((anchor - off - zhi[i]) / 64) on, so
 // L(t) = #{i : T_i <= t} (the D_eff rule at distance anchor - (64 t + off)).
-// advance(t) costs one compare per tile except when a level boundary is crossed.
+// advance(t) costs one compare per tile except when a level boundary is crossed
+// (at most kLevels times per walker), which is laid out as the unlikely path.
 struct LevelWalker {
   int L;
   int next;
@@ -84,7 +85,7 @@ struct LevelWalker {
     next = start_tile(lt, 0);
   }
   __device__ __forceinline__ int advance(const LevelTable& lt, int t) {
-    while (t >= next) {
+    while (__builtin_expect(t >= next, 0)) {
       ++L;
       next = (L < kLevels) ? start_tile(lt, L) : 0x7fffffff;
     }
@@ -373,28 +374,59 @@ __device__ __forceinline__ void qk_stream(const lds_u8* kb, bf16x8 (&f)[kRing], 
   }
 }
 
-// P = exp2(S) of a tile pair packed to bf16 (Pf[p] is the B operand of the PV
-// steps of page p), and the lane's partial row sum of P.  kRaw: S is in raw
-// score units (Q was not scaled) and P = exp2(S * c).
+// The MFMA phase of tile pair u with one level count L for its four 32-key
+// blocks: PV of the previous pair, then QK of this pair, as one straight-line
+// stream (the level counts are known before the phase starts, so nothing
+// branches between its first LDS read and its last MFMA).
+template <int L>
+__device__ __forceinline__ void mfma_phase(const lds_u8* vb, const lds_u8* kb, const bf16x8 (&Pf)[8],
+                                           f32x16 (&O)[4], const u32x4 (&Qf)[kLevels], const f32x16& C,
+                                           f32x16 (&S)[4]) {
+  bf16x8 f[kRing];
+  pv_prefetch(vb, f);
+  pv_stream(vb, kb, Pf, O, f);
+  qk_stream<L>(kb, f, Qf, C, S);
+}
+
+// The MFMA phase of a pair with a level boundary inside it (L0 <= L1 <= L2 <= L3,
+// not all equal): PV as above, then per-tile chains.
+__device__ __forceinline__ void mfma_phase_mixed(int L0, int L1, int L2, int L3, const lds_u8* vb,
+                                                 const lds_u8* kb, const bf16x8 (&Pf)[8], f32x16 (&O)[4],
+                                                 const u32x4 (&Qf)[kLevels], const f32x16& C, f32x16 (&S)[4]) {
+  bf16x8 f[kRing];
+  pv_prefetch(vb, f);
+  pv_stream(vb, kb, Pf, O, f);
+  qk_tile(L0, L1, kb, kb + 8192, Qf, f[32 % kRing], f[33 % kRing], C, S[0], S[1]);
+  qk_tile(L2, L3, kb + 16384, kb + 24576, Qf, f[34 % kRing], f[35 % kRing], C, S[2], S[3]);
+}
+
+// P = exp2(S) of one 32-key block (S[kb]) packed to bf16 (Pf[2kb], Pf[2kb+1]
+// are the B operands of the PV steps of its two pages), added to the lane's
+// partial row sum lt.  kRaw: S is in raw score units (Q was not scaled) and
+// P = exp2(S * c).
+template <bool kRaw>
+__device__ __forceinline__ void exp_block(const f32x16& Sk, bf16x8& P0, bf16x8& P1, float c, float& lt) {
+#pragma unroll
+  for (int hs = 0; hs < 2; ++hs) {
+    u32x4 pk;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float s0 = Sk[8 * hs + 2 * i], s1 = Sk[8 * hs + 2 * i + 1];
+      const float p0 = fast_exp2(kRaw ? s0 * c : s0);
+      const float p1 = fast_exp2(kRaw ? s1 * c : s1);
+      pk[i] = pack_bf16x2(p0, p1);
+      lt += p0 + p1;
+    }
+    (hs == 0 ? P0 : P1) = __builtin_bit_cast(bf16x8, pk);
+  }
+}
+
+// P of the whole tile pair and its partial row sum.
 template <bool kRaw>
 __device__ __forceinline__ float exp_tiles(const f32x16 (&S)[4], bf16x8 (&Pf)[8], float c) {
   float lt = 0.f;
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb) {
-#pragma unroll
-    for (int hs = 0; hs < 2; ++hs) {
-      u32x4 pk;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float s0 = S[kb][8 * hs + 2 * i], s1 = S[kb][8 * hs + 2 * i + 1];
-        const float p0 = fast_exp2(kRaw ? s0 * c : s0);
-        const float p1 = fast_exp2(kRaw ? s1 * c : s1);
-        pk[i] = pack_bf16x2(p0, p1);
-        lt += p0 + p1;
-      }
-      Pf[2 * kb + hs] = __builtin_bit_cast(bf16x8, pk);
-    }
-  }
+  for (int kb = 0; kb < 4; ++kb) exp_block<kRaw>(S[kb], Pf[2 * kb], Pf[2 * kb + 1], c, lt);
   return lt;
 }
 
@@ -546,26 +578,30 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
   // barrier ending its next MFMA phase (steps 2u+2 and 2u+3); both are first
   // read at step 2u+4.  The MFMA phase runs unconditionally (P = 0 when there
   // is nothing to add) so the accumulators stay in place.
-  // the copying group's cache at this kv head and the page stride, computed
-  // once (loop invariants)
+  // The copying group's cache at this kv head and the page stride, computed
+  // once (loop invariants).
   const uint8_t* cbase =
       reinterpret_cast<const uint8_t*>(copies_v ? a.v_cache : a.k_cache) + static_cast<size_t>(kvh) * 4096;
   const uint32_t pstride = static_cast<uint32_t>(a.hkv) * 4096u;
   const int U = T2 >> 1;
+  // Every load issued so far has landed before the loop, so the compiler's
+  // wait counting inside the loop starts from nothing outstanding (it would
+  // otherwise keep a full vector-memory wait in front of the QK stream).
+  __builtin_amdgcn_s_waitcnt(0);
+  // Level counts of the four 32-key blocks of the next MFMA phase, computed in
+  // the softmax phase before it (pair 0: here).
+  int L0 = w_far.advance(a.lt, 0), L1 = w_near.advance(a.lt, 0);
+  int L2 = w_far.advance(a.lt, 1), L3 = w_near.advance(a.lt, 1);
   for (int u = 0; u <= U; ++u) {
     // ---- MFMA phase of pair u ----
     __builtin_amdgcn_s_setprio(1);
     {
       const lds_u8* kb = smem + (u % kPfKPairs) * kPfPairBytes + k_lane;
       const lds_u8* vb = smem + kPfVRegion + ((u + 1) & 1) * kPfPairBytes + v_lane;
-      const int L0 = w_far.advance(a.lt, 2 * u);
-      const int L1 = w_near.advance(a.lt, 2 * u);
-      const int L2 = w_far.advance(a.lt, 2 * u + 1);
-      const int L3 = w_near.advance(a.lt, 2 * u + 1);
       bf16x8 f[kRing];
       pv_prefetch(vb, f);
       pv_stream(vb, kb, Pf, O, f);
-      if (L0 == L3) {  // L0 <= L1 <= L2 <= L3: one level count
+      if (__builtin_expect(L0 == L3, 1)) {  // L0 <= L1 <= L2 <= L3: one level count
         switch (L0) {
           case 8: qk_stream<8>(kb, f, Qf, Cm, S); break;
           case 7: qk_stream<7>(kb, f, Qf, Cm, S); break;
@@ -602,25 +638,20 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
       }
     }
     pf_barrier();
-    {
-      // K (group 0) of tiles 2u+4, 2u+5 into the pair of tiles 2u-2, 2u-1 (read
-      // by both groups in phase u-1), or V (group 1) of tiles 2u+2, 2u+3 into
-      // the pair of tiles 2u-2, 2u-1 (read by both groups' PV in phase u)
-      const int ct = 2 * u + (copies_v ? 2 : 4);
-      const int pa = page_id(a, pg_a), pb = page_id(a, pg_b);
-      lds_u8* dst = copies_v ? smem + kPfVRegion + ((u + 1) & 1) * kPfPairBytes
-                             : smem + ((u + 2) % kPfKPairs) * kPfPairBytes;
-      dst += rank * 4096;
-      const int lim = copies_v ? T2 : T;
-      // whole 1 KB level pairs for K (an odd L also copies level L, which is not read)
-      if (ct < lim) stage_page(cbase, pstride, pa, copies_v ? 4 : (w_ld.advance(a.lt, ct) + 1) >> 1, dst, lane, copy_off);
-      if (ct + 1 < lim)
-        stage_page(cbase, pstride, pb, copies_v ? 4 : (w_ld.advance(a.lt, ct + 1) + 1) >> 1, dst + kPfSlotBytes, lane,
-                   copy_off);
-      pg_a = fetch_page(a, b, 4 * (ct + 2) + rank);
-      pg_b = fetch_page(a, b, 4 * (ct + 3) + rank);
-    }
-    // ---- softmax phase of pair u (lane = query row) ----
+    // ---- softmax phase of pair u (lane = query row), with this wave's copies ----
+    // K (group 0) of tiles 2u+4, 2u+5 into the pair of tiles 2u-2, 2u-1 (read
+    // by both groups in phase u-1), or V (group 1) of tiles 2u+2, 2u+3 into
+    // the pair of tiles 2u-2, 2u-1 (read by both groups' PV in phase u).
+    const int ct = 2 * u + (copies_v ? 2 : 4);
+    const int lim = copies_v ? T2 : T;
+    lds_u8* cdst = (copies_v ? smem + kPfVRegion + ((u + 1) & 1) * kPfPairBytes
+                             : smem + ((u + 2) % kPfKPairs) * kPfPairBytes) + rank * 4096;
+    // whole 1 KB level pairs for K (an odd L also copies level L, which is not read)
+    const int rows_a = copies_v ? 4 : (w_ld.advance(a.lt, ct) + 1) >> 1;
+    const int rows_b = copies_v ? 4 : (w_ld.advance(a.lt, ct + 1) + 1) >> 1;
+    const int pa = page_id(a, pg_a), pb = page_id(a, pg_b);
+    if (ct < lim) stage_page(cbase, pstride, pa, rows_a, cdst, lane, copy_off);
+    if (ct + 1 < lim) stage_page(cbase, pstride, pb, rows_b, cdst + kPfSlotBytes, lane, copy_off);
     if (2 * u < t_end) {
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
@@ -683,6 +714,12 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
 #pragma unroll
       for (int i = 0; i < 8; ++i) Pf[i] = bf16x8{};
     }
+    pg_a = fetch_page(a, b, 4 * (ct + 2) + rank);
+    pg_b = fetch_page(a, b, 4 * (ct + 3) + rank);
+    L0 = w_far.advance(a.lt, 2 * u + 2);
+    L1 = w_near.advance(a.lt, 2 * u + 2);
+    L2 = w_far.advance(a.lt, 2 * u + 3);
+    L3 = w_near.advance(a.lt, 2 * u + 3);
     pf_barrier();
   }
   if (!copies_v) __syncthreads();  // group 0 ends one step late
