@@ -15,6 +15,8 @@ import torch  # noqa: F401  (binds the HIP runtime first, see above)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libatflash_hip.so")
 
+ABI_VERSION = 2
+
 ATF_OK = 0
 ATF_ERR_INVALID = 1
 ATF_ERR_UNSUPPORTED = 2
@@ -23,6 +25,8 @@ ATF_ERR_WORKSPACE = 4
 
 HEAD_DIM = 128
 LEVELS = 8
+SLICES = 16      # 8-dim slices of the vec8 decode table (two per level)
+SLICE_DIMS = 8
 PAGE_SIZE = 16
 LAYOUT_HALF_SPLIT = 0
 LAYOUT_SORTED_PAIR = 1
@@ -48,6 +52,8 @@ SIGNATURES = {
     "atf_decode_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "atf_decode_paged_bf16": (_i, [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i, _p, _i, _p,
                                    _i, _i, _i, _i, _p, _f, _p, _i, _i, _p, _sz, _p]),
+    "atf_decode_paged_slices_bf16": (_i, [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i, _p, _i, _p,
+                                          _i, _i, _i, _i, _p, _f, _p, _i, _i, _p, _sz, _p]),
     "atf_decode_paged_bf16_noalloc": (_i, [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i, _p, _i, _p,
                                            _i, _i, _i, _i, _p, _f, _p, _i, _i, _p]),
     "atf_prefill_tile_levels": (_i, [_p, _i, _i, _i, _p, _p]),
@@ -77,7 +83,7 @@ def lib():
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args
-        if handle.atf_abi_version() != 1:
+        if handle.atf_abi_version() != ABI_VERSION:
             raise RuntimeError("atflash library ABI version mismatch")
         _LIB = handle
     return _LIB
@@ -94,14 +100,18 @@ def check(code):
     raise AtflashError(code, msg)
 
 
-def zhi_array(zhi):
-    """Host int32[LEVELS] for a window table, or None (window OFF)."""
+def zhi_array(zhi, n=LEVELS):
+    """Host int32[n] for a window table (n = LEVELS: the level table; n =
+    SLICES: the per-slice vec8 table), or None (window OFF)."""
     if zhi is None:
         return None
     vals = [int(x) for x in (zhi.tolist() if isinstance(zhi, torch.Tensor) else zhi)]
-    if len(vals) != LEVELS:
-        raise ValueError(f"window table must have {LEVELS} entries (head_dim / 16), got {len(vals)}")
-    return (ctypes.c_int32 * LEVELS)(*vals)
+    if len(vals) != n:
+        raise ValueError(f"window table must have {n} entries (head_dim / {HEAD_DIM // n}), got {len(vals)}")
+    return (ctypes.c_int32 * n)(*vals)
+
+
+K_BLOCK_SHAPE = (SLICES, PAGE_SIZE, SLICE_DIMS)  # one (page, kv head) K block of the cache
 
 
 def ptr(t):

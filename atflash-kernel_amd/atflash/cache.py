@@ -1,12 +1,13 @@
 """Paged KV cache in the kernels' layout (one layer).
 
-    k  bf16 [num_pages, num_kv_heads, 8 levels, 16 tokens, 16 dims]  (RoPE'd K)
-    v  bf16 [num_pages, num_kv_heads, 128 dims, 16 token slots]      (V transposed)
+    k  bf16 [num_pages, num_kv_heads, 16 slices, 16 tokens, 8 dims]  (RoPE'd K)
+    v  bf16 [num_pages, num_kv_heads, 128 dims, 16 token slots]       (V transposed)
 
-A page holds 16 consecutive tokens of one sequence.  K of a page is stored level
-by level (level l = RoPE pairs r in [P-8(l+1), P-8l), dims r and r+P), so the
-window's surviving prefix of a page is one contiguous run and out-of-window
-levels are never fetched.  Pages are zero-initialised.  Sequences own lists of
+A page holds 16 consecutive tokens of one sequence.  K of a page is stored slice
+by slice in wavelength order (slice s = RoPE pairs r in [P-4(s+1), P-4s), dims r
+and r+P; a 16-dim level l is slices 2l and 2l+1), so the window's surviving
+prefix of a page is one contiguous run and out-of-window slices are never
+fetched.  Pages are zero-initialised.  Sequences own lists of
 page ids; page_table() packs them into the int32 [batch, max_pages] table the
 kernels take.
 """
@@ -24,7 +25,7 @@ class PagedKVCache:
         self.num_pages = int(num_pages)
         self.num_kv_heads = int(num_kv_heads)
         self.device = torch.device(device)
-        self.k = torch.zeros((num_pages, num_kv_heads, _lib.LEVELS, PAGE, 16), dtype=torch.bfloat16,
+        self.k = torch.zeros((num_pages, num_kv_heads, *_lib.K_BLOCK_SHAPE), dtype=torch.bfloat16,
                              device=self.device)
         self.v = torch.zeros((num_pages, num_kv_heads, head_dim, PAGE), dtype=torch.bfloat16,
                              device=self.device)

@@ -41,3 +41,19 @@ def decode_s(n_ctx: int, zhi, head_dim: int = 128, block_n: int = 16):
         read += levels_of_zmin(z, zhi)
     s = read / float(levels * n_tiles)
     return s, 2.0 / (1.0 + s)
+
+
+def decode_s_slices(n_ctx: int, zhi_slice, block_n: int = 16):
+    """(s, 2/(1+s)) for one decode step over n_ctx keys with the per-slice
+    (vec8) table, counting the K bytes the decode kernel reads: each 16-key page
+    reads the slices of its youngest key (age (n_ctx-1) - (16p+15)), whatever
+    the per-key rule then masks inside the page."""
+    z = [int(x) for x in (zhi_slice.tolist() if hasattr(zhi_slice, "tolist") else zhi_slice)]
+    n_pages = -(-n_ctx // block_n)
+    read = 0
+    for p in range(n_pages):
+        age = max(0, (n_ctx - 1) - (p * block_n + block_n - 1))
+        read += sum(1 for t in z if t >= age)
+    s = read / float(len(z) * n_pages)
+    return s, 2.0 / (1.0 + s)
+

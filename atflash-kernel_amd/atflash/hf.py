@@ -68,7 +68,7 @@ class PagedLayer(CacheLayerMixin):
         n_pages = owner.batch * owner.pages_per_seq
         self.owner = owner
         self.layer_idx = layer_idx
-        self.k = torch.zeros((n_pages, owner.num_kv_heads, _lib.LEVELS, PAGE, 16), dtype=torch.bfloat16,
+        self.k = torch.zeros((n_pages, owner.num_kv_heads, *_lib.K_BLOCK_SHAPE), dtype=torch.bfloat16,
                              device=owner.device)
         self.v = torch.zeros((n_pages, owner.num_kv_heads, _lib.HEAD_DIM, PAGE), dtype=torch.bfloat16,
                              device=owner.device)

@@ -35,13 +35,18 @@ def _layout_id(layout):
     return LAYOUTS[layout]
 
 
-def _zhi_list(zhi):
+def _zhi_list(zhi, sizes=(_lib.LEVELS,)):
+    """A window table as a list of ints: the level table (LEVELS entries), or for
+    decode also the per-slice vec8 table (SLICES entries)."""
     if zhi is None:
         return None
     vals = [int(x) for x in (zhi.tolist() if isinstance(zhi, torch.Tensor) else zhi)]
-    if len(vals) != _lib.LEVELS:
-        raise ValueError(f"window table must have {_lib.LEVELS} entries, got {len(vals)}")
+    if len(vals) not in sizes:
+        raise ValueError(f"window table must have {' or '.join(map(str, sizes))} entries, got {len(vals)}")
     return vals
+
+
+_DECODE_TABLES = (_lib.LEVELS, _lib.SLICES)
 
 
 def pack_kv(k, v, rope=None, layout="half_split", start_pos=0):
@@ -49,7 +54,7 @@ def pack_kv(k, v, rope=None, layout="half_split", start_pos=0):
     an identity page table.  Returns (k_cache, v_cache, page_table)."""
     B, N, Hkv, D = k.shape
     pages = -(-(int(start_pos) + N) // PAGE)
-    k_cache = torch.empty((B * pages, Hkv, _lib.LEVELS, PAGE, 16), dtype=torch.bfloat16, device=k.device)
+    k_cache = torch.empty((B * pages, Hkv, *_lib.K_BLOCK_SHAPE), dtype=torch.bfloat16, device=k.device)
     v_cache = torch.empty((B * pages, Hkv, D, PAGE), dtype=torch.bfloat16, device=k.device)
     page_table = torch.arange(B * pages, dtype=torch.int32, device=k.device).view(B, pages)
     starts = torch.full((B,), int(start_pos), dtype=torch.int32, device=k.device)
@@ -82,7 +87,9 @@ def _flash_attn_fwd(q, k, v, causal=True, pack_gqa=None, atflash_window_zhi=None
 def single_decode_with_kv_cache(q, k, v, maybe_zhi=None, sm_scale=None, kv_layout="NHD", rope=None,
                                 layout="half_split"):
     """One query token per q head against a contiguous KV (convenience path: the
-    KV is packed into a temporary paged cache first).  Returns o [Hq, 128] bf16."""
+    KV is packed into a temporary paged cache first).  Returns o [Hq, 128] bf16.
+    maybe_zhi: the level table (8 entries, page rule) or the FlashInfer port's
+    per-slice table (16 entries, fiwin_common.zhi_slice_vec8, per-key rule)."""
     if kv_layout == "HND":
         k, v = k.transpose(0, 1), v.transpose(0, 1)
     elif kv_layout != "NHD":
@@ -91,8 +98,8 @@ def single_decode_with_kv_cache(q, k, v, maybe_zhi=None, sm_scale=None, kv_layou
     scale = 1.0 / math.sqrt(q.shape[-1]) if sm_scale is None else float(sm_scale)
     k_cache, v_cache, table = pack_kv(k.unsqueeze(0), v.unsqueeze(0), rope=rope, layout=layout)
     seq = torch.tensor([N], dtype=torch.int32, device=q.device)
-    o = ops.decode_paged(q.unsqueeze(0), k_cache, v_cache, table, seq, N, _zhi_list(maybe_zhi), scale, rope,
-                         _layout_id(layout))
+    o = ops.decode_paged(q.unsqueeze(0), k_cache, v_cache, table, seq, N, _zhi_list(maybe_zhi, _DECODE_TABLES), scale,
+                         rope, _layout_id(layout))
     return o[0]
 
 
@@ -105,5 +112,5 @@ def prefill_paged(q, cache, page_table, nk, q_offset, zhi=None, sm_scale=None, r
 def decode_paged(q, cache, page_table, seq_lens, max_seq_len, zhi=None, sm_scale=None, rope=None,
                  layout="half_split"):
     scale = 1.0 / math.sqrt(q.shape[-1]) if sm_scale is None else float(sm_scale)
-    return ops.decode_paged(q, cache.k, cache.v, page_table, seq_lens, int(max_seq_len), _zhi_list(zhi), scale,
-                            rope, _layout_id(layout))
+    return ops.decode_paged(q, cache.k, cache.v, page_table, seq_lens, int(max_seq_len),
+                            _zhi_list(zhi, _DECODE_TABLES), scale, rope, _layout_id(layout))

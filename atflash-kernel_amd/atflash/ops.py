@@ -30,8 +30,8 @@ def _need(cond, msg):
 
 def _check_cache(k_cache, v_cache):
     _need(k_cache.dtype == torch.bfloat16 and v_cache.dtype == torch.bfloat16, "caches must be bf16")
-    _need(k_cache.dim() == 5 and tuple(k_cache.shape[2:]) == (_lib.LEVELS, _lib.PAGE_SIZE, 16),
-          "k_cache must be [num_pages, num_kv_heads, 8, 16, 16]")
+    _need(k_cache.dim() == 5 and tuple(k_cache.shape[2:]) == _lib.K_BLOCK_SHAPE,
+          "k_cache must be [num_pages, num_kv_heads, 16, 16, 8]")
     _need(v_cache.shape == (k_cache.shape[0], k_cache.shape[1], _lib.HEAD_DIM, _lib.PAGE_SIZE),
           "v_cache must be [num_pages, num_kv_heads, 128, 16]")
     _need(k_cache.is_contiguous() and v_cache.is_contiguous(), "caches must be contiguous")
@@ -136,7 +136,9 @@ def decode_paged(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
                  seq_lens: torch.Tensor, max_seq_len: int, zhi: Optional[List[int]], sm_scale: float,
                  rope_cs: Optional[torch.Tensor], layout: int) -> torch.Tensor:
     """Windowed split-KV decode of q [B, Hq, 128] (query of sequence b at
-    position seq_lens[b] - 1).  Returns out bf16 [B, Hq, 128]."""
+    position seq_lens[b] - 1).  Returns out bf16 [B, Hq, 128].  zhi: the level
+    table (8 entries, page rule) or the per-slice vec8 table (16 entries,
+    per-key rule), None for window OFF."""
     _need_gpu(q, k_cache, v_cache, page_table, seq_lens, rope_cs)
     _check_cache(k_cache, v_cache)
     _need(q.dtype == torch.bfloat16 and q.dim() == 3 and q.shape[-1] == _lib.HEAD_DIM,
@@ -152,10 +154,13 @@ def decode_paged(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
     nbytes = int(L.atf_decode_workspace_bytes(B, Hq, hkv, int(max_seq_len)))
     ws = _decode_workspace(q.device, nbytes)
     out = torch.empty((B, Hq, _lib.HEAD_DIM), dtype=torch.bfloat16, device=q.device)
-    _lib.check(L.atf_decode_paged_bf16(
+    slices = zhi is not None and len(zhi) == _lib.SLICES
+    entry = L.atf_decode_paged_slices_bf16 if slices else L.atf_decode_paged_bf16
+    table = _lib.zhi_array(zhi, _lib.SLICES if slices else _lib.LEVELS)
+    _lib.check(entry(
         _lib.ptr(out), out.stride(0), out.stride(1), _lib.ptr(q), q.stride(0), q.stride(1),
         _lib.ptr(k_cache), _lib.ptr(v_cache), k_cache.shape[0], _lib.ptr(page_table), page_table.shape[1],
-        _lib.ptr(seq_lens.contiguous()), B, Hq, hkv, int(max_seq_len), _lib.zhi_array(zhi), float(sm_scale),
+        _lib.ptr(seq_lens.contiguous()), B, Hq, hkv, int(max_seq_len), table, float(sm_scale),
         _lib.ptr(rope_cs), max_pos, _layout(layout), _lib.ptr(ws), ws.numel() * 4, _lib.stream_of(q.device)))
     return out
 

@@ -61,6 +61,34 @@ int make_table(const int32_t* zhi, atf::LevelTable* t, int64_t longest) {
   return ATF_OK;
 }
 
+// Level table -> the decode kernel's arguments (page rule); the slice table
+// holds each level's entry on its two 8-dim slices.
+int make_decode_table_levels(const int32_t* zhi, atf::DecodeArgs* a, int64_t longest) {
+  if (int r = make_table(zhi, &a->lt, longest)) return r;
+  for (int s = 0; s < atf::kSlices; ++s) a->st.zhi[s] = a->lt.zhi[s / 2];
+  a->per_key = 0;
+  return ATF_OK;
+}
+
+// Per-slice (vec8) table of the FlashInfer window port -> kernel argument,
+// per-key rule (kernels/flashinfer_port/decode.cuh.diff:47-89).  NULL = window
+// OFF.  Entries must be >= 0 and non-increasing (slices in wavelength order, as
+// zhi_slice_vec8 produces them), so that a page's slices are a prefix.  No
+// slice is always read: a key past every slice scores 0, as in the port.
+int make_decode_table_slices(const int32_t* zhi8, atf::DecodeArgs* a) {
+  for (int s = 0; s < atf::kSlices; ++s) a->st.zhi[s] = zhi8 ? zhi8[s] : INT32_MAX;
+  for (int l = 0; l < atf::kLevels; ++l) a->lt.zhi[l] = INT32_MAX;
+  a->per_key = zhi8 ? 1 : 0;  // window OFF runs the level path with every level
+  if (!zhi8) return ATF_OK;
+  for (int s = 0; s < atf::kSlices; ++s) {
+    if (zhi8[s] < 0) return fail(ATF_ERR_INVALID, "zhi_slice[%d] = %d is negative", s, zhi8[s]);
+    if (s > 0 && zhi8[s] > zhi8[s - 1])
+      return fail(ATF_ERR_INVALID, "zhi_slice must be non-increasing (zhi_slice[%d]=%d > zhi_slice[%d]=%d)", s,
+                  zhi8[s], s - 1, zhi8[s - 1]);
+  }
+  return ATF_OK;
+}
+
 int check_layout(int layout, const float* rope_cs, int rope_max_pos) {
   if (layout != ATF_LAYOUT_HALF_SPLIT && layout != ATF_LAYOUT_SORTED_PAIR)
     return fail(ATF_ERR_INVALID, "unknown layout %d", layout);
@@ -209,8 +237,8 @@ namespace {
 int decode_prepare(void* out, int64_t o_sb, int64_t o_sh, const void* q, int64_t q_sb, int64_t q_sh,
                    const void* k_cache, const void* v_cache, int num_pages, const int32_t* page_table, int max_pages,
                    const int32_t* seq_lens, int batch, int num_q_heads, int num_kv_heads, int max_seq_len,
-                   const int32_t* zhi, float sm_scale, const float* rope_cs, int rope_max_pos, int layout,
-                   atf::DecodeArgs* a) {
+                   const int32_t* zhi, bool slice_table, float sm_scale, const float* rope_cs, int rope_max_pos,
+                   int layout, atf::DecodeArgs* a) {
   if (!out || !q || !k_cache || !v_cache || !page_table || !seq_lens)
     return fail(ATF_ERR_INVALID, "null pointer argument");
   if (num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0)
@@ -229,7 +257,9 @@ int decode_prepare(void* out, int64_t o_sb, int64_t o_sh, const void* q, int64_t
     return fail(ATF_ERR_INVALID, "q, caches must be 16-byte and out 8-byte aligned");
   if (q_sb % 8 || q_sh % 8) return fail(ATF_ERR_INVALID, "q strides must be multiples of 8 elements");
   if (o_sb % 4 || o_sh % 4) return fail(ATF_ERR_INVALID, "out strides must be multiples of 4 elements");
-  if (int r = make_table(zhi, &a->lt, static_cast<int64_t>(max_seq_len) - 1)) return r;
+  if (int r = slice_table ? make_decode_table_slices(zhi, a)
+                          : make_decode_table_levels(zhi, a, static_cast<int64_t>(max_seq_len) - 1))
+    return r;
   int ns = 1, pps = 1;
   decode_split(batch, num_kv_heads, max_seq_len, &ns, &pps);
   a->q = static_cast<const uint16_t*>(q);
@@ -259,19 +289,21 @@ int decode_prepare(void* out, int64_t o_sb, int64_t o_sh, const void* q, int64_t
 
 }  // namespace
 
-extern "C" {
+namespace {
 
-int atf_decode_paged_bf16(void* out, int64_t o_sb, int64_t o_sh, const void* q, int64_t q_sb, int64_t q_sh,
+// Decode with a caller-provided workspace, either table kind.
+int decode_with_workspace(void* out, int64_t o_sb, int64_t o_sh, const void* q, int64_t q_sb, int64_t q_sh,
                           const void* k_cache, const void* v_cache, int num_pages, const int32_t* page_table,
                           int max_pages, const int32_t* seq_lens, int batch, int num_q_heads, int num_kv_heads,
-                          int max_seq_len, const int32_t* zhi, float sm_scale, const float* rope_cs,
-                          int rope_max_pos, int layout, void* workspace, size_t workspace_bytes, void* stream) {
+                          int max_seq_len, const int32_t* zhi, bool slice_table, float sm_scale,
+                          const float* rope_cs, int rope_max_pos, int layout, void* workspace,
+                          size_t workspace_bytes, void* stream) {
   if (batch < 0) return fail(ATF_ERR_INVALID, "batch must be >= 0");
   if (batch == 0) return ok();
   atf::DecodeArgs a{};
   if (int r = decode_prepare(out, o_sb, o_sh, q, q_sb, q_sh, k_cache, v_cache, num_pages, page_table, max_pages,
-                             seq_lens, batch, num_q_heads, num_kv_heads, max_seq_len, zhi, sm_scale, rope_cs,
-                             rope_max_pos, layout, &a))
+                             seq_lens, batch, num_q_heads, num_kv_heads, max_seq_len, zhi, slice_table, sm_scale,
+                             rope_cs, rope_max_pos, layout, &a))
     return r;
   const size_t need = partial_bytes(batch, num_kv_heads, a.n_splits);
   if (need > 0 && (!workspace || workspace_bytes < need || !aligned(workspace, 16)))
@@ -285,6 +317,31 @@ int atf_decode_paged_bf16(void* out, int64_t o_sb, int64_t o_sh, const void* q, 
   return ok();
 }
 
+}  // namespace
+
+extern "C" {
+
+int atf_decode_paged_bf16(void* out, int64_t o_sb, int64_t o_sh, const void* q, int64_t q_sb, int64_t q_sh,
+                          const void* k_cache, const void* v_cache, int num_pages, const int32_t* page_table,
+                          int max_pages, const int32_t* seq_lens, int batch, int num_q_heads, int num_kv_heads,
+                          int max_seq_len, const int32_t* zhi, float sm_scale, const float* rope_cs,
+                          int rope_max_pos, int layout, void* workspace, size_t workspace_bytes, void* stream) {
+  return decode_with_workspace(out, o_sb, o_sh, q, q_sb, q_sh, k_cache, v_cache, num_pages, page_table, max_pages,
+                               seq_lens, batch, num_q_heads, num_kv_heads, max_seq_len, zhi, false, sm_scale,
+                               rope_cs, rope_max_pos, layout, workspace, workspace_bytes, stream);
+}
+
+int atf_decode_paged_slices_bf16(void* out, int64_t o_sb, int64_t o_sh, const void* q, int64_t q_sb, int64_t q_sh,
+                                 const void* k_cache, const void* v_cache, int num_pages, const int32_t* page_table,
+                                 int max_pages, const int32_t* seq_lens, int batch, int num_q_heads,
+                                 int num_kv_heads, int max_seq_len, const int32_t* zhi_slice, float sm_scale,
+                                 const float* rope_cs, int rope_max_pos, int layout, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+  return decode_with_workspace(out, o_sb, o_sh, q, q_sb, q_sh, k_cache, v_cache, num_pages, page_table, max_pages,
+                               seq_lens, batch, num_q_heads, num_kv_heads, max_seq_len, zhi_slice, true, sm_scale,
+                               rope_cs, rope_max_pos, layout, workspace, workspace_bytes, stream);
+}
+
 int atf_decode_paged_bf16_noalloc(void* out, int64_t o_sb, int64_t o_sh, const void* q, int64_t q_sb, int64_t q_sh,
                                   const void* k_cache, const void* v_cache, int num_pages,
                                   const int32_t* page_table, int max_pages, const int32_t* seq_lens, int batch,
@@ -294,8 +351,8 @@ int atf_decode_paged_bf16_noalloc(void* out, int64_t o_sb, int64_t o_sh, const v
   if (batch == 0) return ok();
   atf::DecodeArgs a{};
   if (int r = decode_prepare(out, o_sb, o_sh, q, q_sb, q_sh, k_cache, v_cache, num_pages, page_table, max_pages,
-                             seq_lens, batch, num_q_heads, num_kv_heads, max_seq_len, zhi, sm_scale, rope_cs,
-                             rope_max_pos, layout, &a))
+                             seq_lens, batch, num_q_heads, num_kv_heads, max_seq_len, zhi, false, sm_scale,
+                             rope_cs, rope_max_pos, layout, &a))
     return r;
   const size_t partial = partial_bytes(batch, num_kv_heads, a.n_splits);
   if (partial > atf::kDecScratchBytes)

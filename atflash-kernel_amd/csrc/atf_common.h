@@ -12,12 +12,18 @@
 //   zhi the per-level table of window_tables/atflash_window.py:85-108; window OFF
 //   is zhi[i] = INT32_MAX, i.e. D_eff = d everywhere.
 //
+//   The decode kernel also takes the finer table of the FlashInfer window port
+//   (kernels/flashinfer_port/fiwin_common.py:35-47): 16 slices of 8 dims, slice s
+//   = 4 pairs in wavelength order (pairs r in [P-4(s+1), P-4s)), read for key
+//   ages z <= zhi8[s]; level l is slices 2l and 2l+1.
+//
 // Paged KV cache (one layer), page = 16 tokens, per (page, kv head):
-//   K block  [8 levels][16 tokens][16 dims] bf16 = 4096 B, RoPE already applied.
-//            Dims of a level are stored as [first-half 8 | second-half 8]
-//            (half-split) or [16l .. 16l+15] (sorted pair).  Levels are
-//            contiguous 512 B runs, so a page read for L levels is one
-//            contiguous 512*L-byte prefix of the block.
+//   K block  [16 slices][16 tokens][8 dims] bf16 = 4096 B, RoPE already applied.
+//            The dims of slice s are stored as [first-half 4 | second-half 4]
+//            (half-split: dims [P-4(s+1), P-4s) then the same + P) or
+//            [8s .. 8s+7] (sorted pair).  Slices are contiguous 256 B runs in
+//            wavelength order, so a page read for n slices (L levels = 2L
+//            slices) is one contiguous 256*n-byte prefix of the block.
 //   V block  [128 dims][16 token slots] bf16 = 4096 B (V transposed), token t of
 //            the page stored in slot kVSlot(t); the slot order matches the lane
 //            layout of the 32x32x16 and 16x16x16 MFMA accumulators so that P never
@@ -32,8 +38,10 @@ namespace atf {
 constexpr int kD = 128;
 constexpr int kP = 64;
 constexpr int kLevels = 8;
+constexpr int kSlices = 16;    // 8-dim slices, two per level
+constexpr int kSliceDims = 8;
 constexpr int kPage = 16;
-constexpr int kBlockElems = kLevels * kPage * 16;  // 2048 bf16 = 4096 B
+constexpr int kBlockElems = kSlices * kPage * kSliceDims;  // 2048 bf16 = 4096 B
 constexpr int kLayoutHalfSplit = 0;
 constexpr int kLayoutSortedPair = 1;
 
@@ -60,12 +68,33 @@ __device__ __forceinline__ int levels_of(const LevelTable& t, int z) {
   return n < 1 ? 1 : n;
 }
 
-// First dim of the two 8-dim chunks of level l.
+// The per-slice distance table of the decode kernel (kernel argument, SGPRs).
+struct SliceTable {
+  int32_t zhi[kSlices];
+};
+
+// First dim of the two 8-dim chunks of level l in the input row (half-split:
+// the first-half and second-half dims of the level's 8 pairs).
 __device__ __forceinline__ int level_chunk0(int layout, int l) {
   return layout == kLayoutHalfSplit ? kP - 8 * (l + 1) : 16 * l;
 }
 __device__ __forceinline__ int level_chunk1(int layout, int l) {
   return layout == kLayoutHalfSplit ? 2 * kP - 8 * (l + 1) : 16 * l + 8;
+}
+
+// First pair (half-split: first dim) of slice s: pairs r in [P-4(s+1), P-4s).
+__device__ __forceinline__ int slice_pair0(int s) { return kP - 4 * (s + 1); }
+
+// The 8 dims of slice s of an input row, in the order the cache stores them:
+// half-split [x1 of the slice's 4 pairs | x2 of the same pairs] (two 8-byte
+// loads), sorted pair dims [8s, 8s+8) (one 16-byte load).
+__device__ __forceinline__ u32x4 load_slice(const uint16_t* row, int layout, int s) {
+  if (layout == kLayoutHalfSplit) {
+    const u32x2 x1 = *reinterpret_cast<const u32x2*>(row + slice_pair0(s));
+    const u32x2 x2 = *reinterpret_cast<const u32x2*>(row + kP + slice_pair0(s));
+    return u32x4{x1[0], x1[1], x2[0], x2[1]};
+  }
+  return *reinterpret_cast<const u32x4*>(row + 8 * s);
 }
 
 // Slot of token t (0..15) inside a transposed V page: token groups of 4 are
@@ -125,6 +154,21 @@ __device__ __forceinline__ u32x4 rope_half(const u32x4& x1v, const u32x4& x2v, c
   return pack8(y);
 }
 
+// Rotate-half RoPE on one half-split slice x = [x1 of 4 pairs | x2 of the same
+// pairs]: [x1 c - x2 s | x2 c + x1 s], times `scale`.  cs holds (cos, sin) per
+// pair.
+__device__ __forceinline__ u32x4 rope_slice(const u32x4& x, const float* cs, float scale = 1.f) {
+  float v[8], y[8];
+  unpack8(x, v);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float c = cs[2 * i], s = cs[2 * i + 1];
+    y[i] = scale * (v[i] * c - v[4 + i] * s);
+    y[4 + i] = scale * (v[4 + i] * c + v[i] * s);
+  }
+  return pack8(y);
+}
+
 __device__ __forceinline__ u32x4 ldg16(const void* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }
@@ -133,6 +177,19 @@ __device__ __forceinline__ void load_cs8(const float* rope_cs, int pos, int pair
   const u32x4* p = reinterpret_cast<const u32x4*>(rope_cs + (static_cast<size_t>(pos) * kP + pair0) * 2);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
+    const u32x4 v = p[i];
+    cs[4 * i + 0] = __uint_as_float(v[0]);
+    cs[4 * i + 1] = __uint_as_float(v[1]);
+    cs[4 * i + 2] = __uint_as_float(v[2]);
+    cs[4 * i + 3] = __uint_as_float(v[3]);
+  }
+}
+
+// (cos, sin) of the 4 pairs starting at pair0, at position pos.
+__device__ __forceinline__ void load_cs4(const float* rope_cs, int pos, int pair0, float* cs) {
+  const u32x4* p = reinterpret_cast<const u32x4*>(rope_cs + (static_cast<size_t>(pos) * kP + pair0) * 2);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
     const u32x4 v = p[i];
     cs[4 * i + 0] = __uint_as_float(v[0]);
     cs[4 * i + 1] = __uint_as_float(v[1]);

@@ -1,4 +1,4 @@
-// Windowed split-KV decode over the paged, level-blocked KV cache (gfx950).
+// Windowed split-KV decode over the paged, slice-blocked KV cache (gfx950).
 //
 // Replaces the FlashInfer window port's single-request decode
 // (single_decode_with_kv_cache_with_jit_module(..., maybe_zhi_slice=...),
@@ -7,18 +7,23 @@
 //
 // One workgroup of 8 waves per (sequence, kv head, split of pages); each wave
 // streams its own pages.  The G = Hq/Hkv query heads of the kv head are the 16
-// columns of v_mfma_f32_16x16x32_bf16 (S^T = K Q^T, two 16-dim levels per
+// columns of v_mfma_f32_16x16x32_bf16 (S^T = K Q^T, four 8-dim slices per
 // instruction) and v_mfma_f32_16x16x16_bf16 (O^T = V^T P^T, 16 tokens per
 // instruction).  K and V are loaded straight into the MFMA operand registers.
-// The window predicate is per page: page p is read for its first
-// L(p) = D_eff/16 levels, D_eff = 16 * #{i : zhi[i] >= (N-1) - (16p+15)}; the
-// loads of the other levels are never issued, so out-of-window K bytes are not
-// read from HBM.
+// The window table is per 8-dim slice (16 entries; a 16-dim level table is
+// passed as each level's value for its two slices).  Page p is read for the
+// first n(p) = #{s : zhi8[s] >= (N-1) - (16p+15)} slices, those its youngest
+// key reads; the loads of the other slices are never issued, so out-of-window
+// K bytes are not read from HBM.  Page rule (level table, block_n = 16): every
+// key of the page uses those slices.  Per-key rule (vec8 table, as the
+// FlashInfer port's decode, kernels/flashinfer_port/decode.cuh.diff:47-89):
+// on a page with a slice boundary inside it, an older key's out-of-window
+// slices are zeroed in registers before the MFMA.
 //
 // Merging: the 8 wave partials (m, l, o) of a split are combined in LDS.  With
 // one split per (sequence, kv head) the workgroup writes the output itself.
 // Otherwise it stores the split's partial in the workspace and ends, and a
-// second kernel (decode_merge_kernel, one workgroup per (sequence, kv head))
+// second kernel (decode_merge_kernel, four workgroups per (sequence, kv head))
 // merges the split partials by log-sum-exp and writes the output.  The kernel
 // boundary orders the partial stores before the merge loads, so no workgroup
 // waits on another inside a launch: no arrival counters, atomics or fences.
@@ -50,10 +55,10 @@ __device__ __forceinline__ float quad_sum(float x) {
 }
 
 struct PageRegs {
-  u32x4 k[4];  // level pairs
+  u32x4 k[4];  // slice quads (32 dims each)
   u32x2 v[8];  // 16-row d blocks
-  int L;
   int n0;
+  bool mask;   // per-key rule with a slice boundary inside the page
 };
 
 // Page-table entries of the kDecUnroll pages starting at p0, in vector
@@ -75,28 +80,71 @@ __device__ __forceinline__ void dec_fetch_group(const DecodeArgs& a, int b, int 
   }
 }
 
-// K and V operands of page p whose page-table entry is `raw`.
-__device__ __forceinline__ void dec_load_page(const DecodeArgs& a, int h, int raw, int p, int N, int lane,
+// Slice count of a key at a fixed offset in its page as the page index p walks
+// up (per-slice table, per-key rule): slice s is read from page
+// P_s = ceil((anchor - zhi8[s]) / 16) on, anchor = N-1 - offset, so
+// n(p) = #{s : P_s <= p}.  advance(p) costs one compare per page except when a
+// slice boundary is crossed (at most 16 times), laid out as the unlikely path.
+struct SliceWalker {
+  int n;
+  int next;
+  int anchor;
+  __device__ __forceinline__ int start_page(const SliceTable& st, int s) const {
+    const int z = min(st.zhi[s], 1 << 30);
+    return (anchor - z + kPage - 1) >> 4;  // ceil((anchor - zhi) / 16), arithmetic shift
+  }
+  __device__ __forceinline__ void init(const SliceTable& st, int anchor_) {
+    anchor = anchor_;
+    n = 0;
+    next = start_page(st, 0);
+  }
+  __device__ __forceinline__ int advance(const SliceTable& st, int p) {
+    while (__builtin_expect(p >= next, 0)) {
+      ++n;
+      next = (n < kSlices) ? start_page(st, n) : 0x7fffffff;
+    }
+    return n;
+  }
+};
+
+// The slices page p reads and whether an older key of it reads fewer.  Page
+// rule (level table): 2 L(p) slices, L(p) = levels of the youngest key's age.
+// Per-key rule: the youngest key's slices; a slice boundary falls inside the
+// page when the oldest key's count differs.
+template <bool kPerKey>
+__device__ __forceinline__ void page_slices(const DecodeArgs& a, SliceWalker& young, SliceWalker& old, int p, int N,
+                                            int& ns, bool& mask) {
+  if constexpr (kPerKey) {
+    ns = young.advance(a.st, p);
+    mask = old.advance(a.st, p) != ns;
+  } else {
+    ns = 2 * levels_of(a.lt, max(0, (N - 1) - (p * kPage + kPage - 1)));
+    mask = false;
+  }
+}
+
+// K and V operands of page p whose page-table entry is `raw`, reading its first
+// ns slices of K.
+__device__ __forceinline__ void dec_load_page(const DecodeArgs& a, int h, int raw, int p, int ns, bool mask, int lane,
                                               PageRegs& r) {
   r.n0 = p * kPage;
-  r.L = levels_of(a.lt, max(0, (N - 1) - (r.n0 + kPage - 1)));
+  r.mask = mask;
   const int pg = __builtin_amdgcn_readfirstlane(raw);
   const bool ok = pg >= 0 && pg < a.num_pages;
   // The page's K and V blocks as range-checked buffer resources: a load at or
-  // past the range returns zeros without a memory request.  K's levels are a
-  // contiguous prefix of its block, so a range of L(p) * 512 bytes reads the
-  // in-window levels and yields zeros for the others (lanes 32-63 of an odd
-  // level pair included); an invalid page entry gets an empty range.  The
-  // loads are therefore unconditional: wave-uniform base, 32-bit lane offset,
-  // immediate row offset, no per-load address arithmetic.
+  // past the range returns zeros without a memory request.  K's slices are a
+  // contiguous prefix of its block, so a range of ns * 256 bytes reads the
+  // in-window slices and yields zeros for the others; an invalid page entry
+  // gets an empty range.  The loads are therefore unconditional: wave-uniform
+  // base, 32-bit lane offset, immediate row offset, no per-load address
+  // arithmetic.
   const size_t blk_bytes = (static_cast<size_t>(ok ? pg : 0) * a.hkv + h) * (kBlockElems * 2);
   const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(a.k_cache) + blk_bytes / 2, 0, ok ? r.L * (kPage * 16 * 2) : 0, kBufferWord3);
+      const_cast<uint16_t*>(a.k_cache) + blk_bytes / 2, 0, ok ? ns * (kPage * kSliceDims * 2) : 0, kBufferWord3);
   const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(a.v_cache) + blk_bytes / 2, 0, ok ? kBlockElems * 2 : 0, kBufferWord3);
-  // K: level 2lp + lane/32, token lane%16, half (lane/16)%2 of the level's 16 dims
-  const uint32_t koff = (static_cast<uint32_t>(lane >> 5) << 9) | (static_cast<uint32_t>(lane & 15) << 5) |
-                        (static_cast<uint32_t>((lane >> 4) & 1) << 4);
+  // K: slice 4 lp + lane/16, token lane%16: quad lp is the 1 KB run at lp * 1024
+  const uint32_t koff = static_cast<uint32_t>(lane) << 4;
 #pragma unroll
   for (int lp = 0; lp < 4; ++lp)
     r.k[lp] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, koff + lp * 1024u, 0, 0));
@@ -110,6 +158,7 @@ __device__ __forceinline__ void dec_load_page(const DecodeArgs& a, int h, int ra
 }
 
 // two waves per SIMD: at most 256 registers per wave
+template <bool kPerKey>
 __global__ __launch_bounds__(kDecWaves * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void decode_kernel(DecodeArgs a) {
   // wave partials
@@ -135,39 +184,54 @@ void decode_kernel(DecodeArgs a) {
   int ent[kDecUnroll];
   PageRegs pr[kDecUnroll];
   const int p_first = p_begin + kDecUnroll * __builtin_amdgcn_readfirstlane(wave);
+  // per-key rule: slice walkers for the youngest (offset 15) and oldest key of a page
+  SliceWalker wy, wo;
+  if constexpr (kPerKey) {
+    wy.init(a.st, (N - 1) - (kPage - 1));
+    wo.init(a.st, N - 1);
+  }
   if (p_first < p_end) {
     dec_fetch_group(a, b, p_first, p_begin, p_end, ent);
 #pragma unroll
     for (int u = 0; u < kDecUnroll; ++u) {
-      if (p_first + u < p_end) dec_load_page(a, h, ent[u], p_first + u, N, lane, pr[u]);
+      if (p_first + u < p_end) {
+        int ns;
+        bool mask;
+        page_slices<kPerKey>(a, wy, wo, p_first + u, N, ns, mask);
+        dec_load_page(a, h, ent[u], p_first + u, ns, mask, lane, pr[u]);
+      }
     }
     dec_fetch_group(a, b, p_first + kStride, p_begin, p_end, ent);
   }
 
-  // ---- Q^T fragments: lane holds q head g, level 2lp + lane/32, half (lane/16)%2 ----
+  // ---- Q^T fragments: lane holds q head g, slice 4 lp + lane/16 ----
   u32x4 Qf[4];
   {
     const int qh = h * a.group + g;
     const bool valid = g < a.group && N > 0;
     const uint16_t* qrow = a.q + static_cast<int64_t>(b) * a.q_sb + static_cast<int64_t>(qh) * a.q_sh;
-    const bool second = ((lane >> 4) & 1) != 0;
 #pragma unroll
     for (int lp = 0; lp < 4; ++lp) {
       u32x4 v = {0u, 0u, 0u, 0u};
-      const int level = 2 * lp + (lane >> 5);
+      const int sl = 4 * lp + (lane >> 4);
       if (valid) {
-        const int c0 = level_chunk0(a.layout, level);
-        const int c1 = level_chunk1(a.layout, level);
+        v = load_slice(qrow, a.layout, sl);
         if (a.rope_cs != nullptr) {
-          float cs[16];
-          load_cs8(a.rope_cs, N - 1, c0, cs);
-          v = rope_half(ldg16(qrow + c0), ldg16(qrow + c1), cs, second);
-        } else {
-          v = ldg16(qrow + (second ? c1 : c0));
+          float cs[8];
+          load_cs4(a.rope_cs, N - 1, slice_pair0(sl), cs);
+          v = rope_slice(v, cs);
         }
       }
       Qf[lp] = v;
     }
+  }
+  // per-key rule: the distance limit of this lane's slice in each quad
+  int zl[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int lp = 0; lp < 4 && kPerKey; ++lp) {
+    const int sg = lane >> 4;
+    const int z0 = a.st.zhi[4 * lp], z1 = a.st.zhi[4 * lp + 1], z2 = a.st.zhi[4 * lp + 2], z3 = a.st.zhi[4 * lp + 3];
+    zl[lp] = sg == 0 ? z0 : (sg == 1 ? z1 : (sg == 2 ? z2 : z3));
   }
 
   f32x4 O[8];
@@ -180,7 +244,15 @@ void decode_kernel(DecodeArgs a) {
     for (int u = 0; u < kDecUnroll; ++u) {
       if (p0 + u >= p_end) break;
       PageRegs& r = pr[u];
-      // all four level pairs: the out-of-window levels were loaded as zeros and
+      if (kPerKey && r.mask) {
+        // a slice boundary inside the page: a key older than its slice's limit
+        // (age > zhi8[slice]) drops that slice (lane: key lane%16, slice 4 lp + lane/16)
+        const int age = (N - 1) - (r.n0 + (lane & 15));
+#pragma unroll
+        for (int lp = 0; lp < 4; ++lp)
+          if (age > zl[lp]) r.k[lp] = u32x4{0u, 0u, 0u, 0u};
+      }
+      // all four slice quads: the out-of-window slices were loaded as zeros and
       // add exact zeros (cheaper than branching around their MFMAs)
       f32x4 S = f32x4{};
 #pragma unroll
@@ -239,7 +311,12 @@ void decode_kernel(DecodeArgs a) {
     if (pn < p_end) {
 #pragma unroll
       for (int u = 0; u < kDecUnroll; ++u) {
-        if (pn + u < p_end) dec_load_page(a, h, ent[u], pn + u, N, lane, pr[u]);
+        if (pn + u < p_end) {
+          int ns;
+          bool mask;
+          page_slices<kPerKey>(a, wy, wo, pn + u, N, ns, mask);
+          dec_load_page(a, h, ent[u], pn + u, ns, mask, lane, pr[u]);
+        }
       }
       dec_fetch_group(a, b, pn + kStride, p_begin, p_end, ent);
     }
@@ -382,7 +459,9 @@ __global__ __launch_bounds__(kDecWaves * 64) void decode_merge_kernel(DecodeArgs
   }
 }
 
-// Level count per page for one sequence of length N (decode rule, block_n = 16).
+// Level count per page for one sequence of length N under the page rule
+// (block_n = 16), as page_slices<false> computes it (the kernel reads twice as
+// many 8-dim slices).
 __global__ void decode_page_levels_kernel(int32_t* out, int n_pages, int N, LevelTable lt) {
   const int p = blockIdx.x * blockDim.x + threadIdx.x;
   if (p >= n_pages) return;
@@ -391,7 +470,10 @@ __global__ void decode_page_levels_kernel(int32_t* out, int n_pages, int N, Leve
 
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t s) {
   if (a.batch <= 0) return hipSuccess;
-  hipLaunchKernelGGL(decode_kernel, dim3(a.n_splits, a.hkv, a.batch), dim3(kDecWaves * 64), 0, s, a);
+  if (a.per_key)
+    hipLaunchKernelGGL(decode_kernel<true>, dim3(a.n_splits, a.hkv, a.batch), dim3(kDecWaves * 64), 0, s, a);
+  else
+    hipLaunchKernelGGL(decode_kernel<false>, dim3(a.n_splits, a.hkv, a.batch), dim3(kDecWaves * 64), 0, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.n_splits == 1) return e;
   hipLaunchKernelGGL(decode_merge_kernel, dim3(kMergeChunks, a.hkv, a.batch), dim3(kDecWaves * 64), 0, s, a);

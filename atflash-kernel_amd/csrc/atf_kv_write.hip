@@ -1,11 +1,12 @@
-// Paged KV-cache writer: RoPE on K at write time, level-blocked K pages and
+// Paged KV-cache writer: RoPE on K at write time, slice-blocked K pages and
 // transposed V pages (the cache format both attention kernels read).
 //
 // Replaces the reference's two steps around the cache: the RoPE + head-dim
 // permutation patch (e2e_pipeline/atflash_e2e_fafi.py:186-192) and the HF cache
 // append the kernels then read (e2e_pipeline/atflash_e2e_fafi.py:101-119).
 // The permutation is not needed here: the cache stores the half-split dims of
-// each 16-dim level contiguously, so the window stays a prefix of every page.
+// each 8-dim slice (4 pairs) contiguously, in wavelength order, so the window
+// stays a prefix of every page.
 #include "atf_launch.h"
 
 namespace atf {
@@ -13,9 +14,9 @@ namespace atf {
 // One workgroup of 128 threads per (cache page, sequence): it writes the
 // page's slots that the call covers, for every kv head, kKvwHeads heads per
 // pass, so the RoPE (cos, sin) row of each position is read once for all of
-// them.  K: thread (level l = tid/16, slot tid%16) loads its token's level l of
-// every head of the pass, then rotates and writes each 32 B row, so a wave
-// writes four whole 512 B level blocks per head.  V: the page's token rows of
+// them.  K: thread (level l = tid/16, slot tid%16) loads its token's level l
+// (slices 2l, 2l+1) of every head of the pass, then rotates it and writes the
+// two 16 B slice rows, so a wave writes eight whole 256 B slice blocks per head.  V: the page's token rows of
 // the pass's heads are staged in LDS with 16-byte loads, then thread d writes
 // V^T row d of each head (32 B: 16 slots in the {0,2,1,3} group order) with
 // two 16-byte stores.  A page the call covers only in part (the first and last
@@ -75,9 +76,17 @@ __global__ __launch_bounds__(128) void kv_write_kernel(KvWriteArgs a) {
             y1 = rope_half(x1[j], x2[j], cs, false);
             y2 = rope_half(x1[j], x2[j], cs, true);
           }
-          uint16_t* kdst = a.k_cache + blk0 + static_cast<size_t>(h0 + j) * kBlockElems + l * 256 + slot * 16;
-          *reinterpret_cast<u32x4*>(kdst) = y1;
-          *reinterpret_cast<u32x4*>(kdst + 8) = y2;
+          // half-split: y1 / y2 hold the first / second halves of the level's 8
+          // pairs in ascending pair order; slice 2l is the upper 4 pairs (the
+          // longer wavelengths), slice 2l+1 the lower 4.  Sorted pair: the two
+          // 8-dim chunks are the slices.
+          const bool hs = a.layout == kLayoutHalfSplit;
+          const u32x4 sa = hs ? u32x4{y1[2], y1[3], y2[2], y2[3]} : y1;
+          const u32x4 sb = hs ? u32x4{y1[0], y1[1], y2[0], y2[1]} : y2;
+          uint16_t* kdst = a.k_cache + blk0 + static_cast<size_t>(h0 + j) * kBlockElems +
+                           (2 * l) * (kPage * kSliceDims) + slot * kSliceDims;
+          *reinterpret_cast<u32x4*>(kdst) = sa;
+          *reinterpret_cast<u32x4*>(kdst + kPage * kSliceDims) = sb;
         }
       }
     }

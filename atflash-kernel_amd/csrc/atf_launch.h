@@ -76,7 +76,13 @@ struct DecodeArgs {
   float scale_log2;
   const float* rope_cs;
   int layout;
+  // Window.  per_key = 0: the level table lt, page rule (block_n = 16): every
+  // key of a page reads the 2 L levels' slices of its youngest key, L >= 1.
+  // per_key = 1: the per-slice (vec8) table st, slice s of a key at age z read
+  // iff z <= st.zhi[s] (the FlashInfer port's rule, no minimum).
   LevelTable lt;
+  SliceTable st;
+  int per_key;
   float* ws_ml;        // [B][Hkv][n_splits][16][2]   split partials (n_splits > 1)
   float* ws_o;         // [B][Hkv][n_splits][16][128]
 };

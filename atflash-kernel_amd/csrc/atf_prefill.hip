@@ -122,17 +122,16 @@ __device__ __forceinline__ int page_id(const PrefillArgs& a, int raw) {
 
 // LDS layout of a staged page.  An MFMA A operand is read with ds_read_b128,
 // lane l taking 16 bytes of row l%32 (half l/32 of the 16-element k slice).
-// The cache rows are 32 bytes long (16 keys of a V^T row, 16 dims of a K level
-// row), so reading them in place puts lanes j and j+4 of every 8-lane group on
-// the same LDS banks.  The staging copy therefore permutes the 16-byte chunks
-// of each 1 KB copy (its source address is per lane): LDS chunk i of a copy
-// holds half (i/16)%2 of K row i%16 of level i/32, resp. half i/32 of V^T row
-// i%32.  Every operand read is then 64 consecutive 16-byte chunks per half:
+// Read in place, rows 32 bytes long would put lanes j and j+4 of every 8-lane
+// group on the same LDS banks; every operand read is instead 64 consecutive
+// 16-byte chunks per half:
 //   K   level lv, token tk, half hf:  lv*512 + hf*256 + tk*16
 //   V^T row d (1 KB block d/32), half hf:  (d/32)*1024 + hf*512 + (d%32)*16
-__device__ __forceinline__ int k_copy_src(int lane) {
-  return ((lane >> 5) << 9) + ((lane & 15) << 5) + (((lane >> 4) & 1) << 4);
-}
+// For K this is the cache's own page layout (slice 2lv + hf, token tk), so a
+// copy is contiguous.  The V^T rows of the cache are 32 bytes long (16 keys),
+// so the V copy permutes the 16-byte chunks of each 1 KB copy (its source
+// address is per lane): LDS chunk i holds half i/32 of V^T row i%32.
+__device__ __forceinline__ int k_copy_src(int lane) { return lane << 4; }
 __device__ __forceinline__ int v_copy_src(int lane) { return ((lane & 31) << 5) + ((lane >> 5) << 4); }
 // Byte offset of V^T element (dim d, slot s) in a staged page.
 __device__ __forceinline__ int v_lds_elem(int d, int s) {
@@ -484,14 +483,13 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
     for (int l = 0; l < kLevels; ++l) {
       u32x4 v = {0u, 0u, 0u, 0u};
       if (row < a.nq) {
-        const int c0 = level_chunk0(a.layout, l);
-        const int c1 = level_chunk1(a.layout, l);
+        // k half h of level l is slice 2l + h, as in the cache's K pages
+        const int sl = 2 * l + (second ? 1 : 0);
+        v = load_slice(qrow, a.layout, sl);
         if (a.rope_cs != nullptr) {
-          float cs[16];
-          load_cs8(a.rope_cs, a.q_offset + row, c0, cs);
-          v = rope_half(ldg16(qrow + c0), ldg16(qrow + c1), cs, second, a.scale_log2);
-        } else {
-          v = ldg16(qrow + (second ? c1 : c0));
+          float cs[8];
+          load_cs4(a.rope_cs, a.q_offset + row, slice_pair0(sl), cs);
+          v = rope_slice(v, cs, a.scale_log2);
         }
       }
       Qf[l] = v;

@@ -96,7 +96,7 @@ def _stats(ts):
 
 def bench_gpu(args):
     import torch
-    from atflash import atflash_window as AW, interface, ops, rope as R
+    from atflash import atflash_window as AW, fiwin_common as FW, interface, ops, rope as R
     from atflash.cache import PagedKVCache
 
     dev = torch.device("cuda:0")
@@ -155,7 +155,11 @@ def bench_gpu(args):
     seq = torch.tensor([N], dtype=torch.int32, device=dev)
     del q, k, v
     torch.cuda.empty_cache()
-    for name, zhi in (windows.items() if args.only in ("all", "decode") else []):
+    # decode also with the FlashInfer port's per-slice (vec8) table, per-key rule
+    dec_windows = dict(windows)
+    for name, k_ret in (("k2_vec8", 2.0), ("k64_vec8", 64.0)):
+        dec_windows[name] = FW.zhi_slice_vec8(D, BASE, k_ret).tolist()
+    for name, zhi in (dec_windows.items() if args.only in ("all", "decode") else []):
         zl = None if zhi is None else list(zhi)
         it = [0]
 
@@ -310,7 +314,8 @@ def slice_ratios(N):
         zhi = AW.window_zhi_from_kret(D, BASE, k_ret, 1 << 23)
         st = AW.slice_stats("prefill", N, N, 32, 32, zhi, D)
         s_dec, _ = FW.decode_s(N, zhi, D, 16)
-        out[name] = {"s_prefill": st["qk_slice_ratio"], "s_decode": s_dec}
+        s_vec8, _ = FW.decode_s_slices(N, FW.zhi_slice_vec8(D, BASE, k_ret), 16)
+        out[name] = {"s_prefill": st["qk_slice_ratio"], "s_decode": s_dec, "s_decode_vec8": s_vec8}
     return out
 
 
@@ -434,8 +439,13 @@ def main():
         t = attn[name]["mean_ms"] * 1e-3
         roof[name] = {"flops": fl, "tflops": fl / t / 1e12, "frac": fl / t / PEAK_BF16}
     dec = {}
-    for name in ("off", "k2", "k64"):
-        s = 1.0 if name == "off" else sr[name]["s_decode"]
+    for name in res["decode"]:
+        if name == "off":
+            s = 1.0
+        elif name.endswith("_vec8"):
+            s = sr[name[:-5]]["s_decode_vec8"]
+        else:
+            s = sr[name]["s_decode"]
         nbytes = N * HKV * D * 2 * (1.0 + s) + HQ * D * 4
         t = res["decode"][name]["batch_mean_ms"] * 1e-3
         dec[name] = {"bytes": nbytes, "GBps": nbytes / t / 1e9, "frac": nbytes / t / PEAK_HBM,
@@ -497,10 +507,10 @@ def main():
             "decode_us_per_call_median": {n: res["decode"][n]["median_ms"] * 1e3 for n in res["decode"]},
             "prefill_on_over_off": {n: pre["off"]["median_ms"] / pre[n]["median_ms"] for n in ("k2", "k64")},
             "decode_on_over_off": {n: res["decode"]["off"]["batch_mean_ms"] / res["decode"][n]["batch_mean_ms"]
-                                   for n in ("k2", "k64")},
+                                   for n in res["decode"] if n != "off"},
             "slice_ratios": sr,
-            "ceilings": {n: {"prefill": 2 / (1 + sr[n]["s_prefill"]), "decode": 2 / (1 + sr[n]["s_decode"])}
-                         for n in sr},
+            "ceilings": {n: {"prefill": 2 / (1 + sr[n]["s_prefill"]), "decode": 2 / (1 + sr[n]["s_decode"]),
+                             "decode_vec8": 2 / (1 + sr[n]["s_decode_vec8"])} for n in sr},
             "kv_write_us": kvw["us_per_launch"],
             "decode_pool_bytes": res["decode_pool_bytes"],
             "timed_region_wall_s": wall,

@@ -16,9 +16,16 @@
  * would drop levels the rule keeps.  NULL means window OFF: plain causal attention,
  * every level read at every distance.  Level l holds RoPE pairs
  * r in [64-8(l+1), 64-8l) (dims r and r+64 of the half-split layout).
+ * The decode also takes the FlashInfer window port's finer table `zhi_slice`
+ * (atf_decode_paged_slices_bf16): ATF_SLICES int32 entries, zhi_slice[s] the
+ * largest key age (seq_len - 1 - position) at which 8-dim slice s (RoPE pairs
+ * r in [64-4(s+1), 64-4s), four pairs in wavelength order) is still read
+ * (kernels/flashinfer_port/fiwin_common.py:35-47); level l is slices 2l, 2l+1.
  *
  * Paged KV cache (one layer): pages of ATF_PAGE_SIZE = 16 tokens.
- *   k_cache  bf16 [num_pages][num_kv_heads][8 levels][16 tokens][16 dims]
+ *   k_cache  bf16 [num_pages][num_kv_heads][16 slices][16 tokens][8 dims]
+ *            (slice s: half-split dims [64-4(s+1), 64-4s) then the same + 64;
+ *            sorted pair dims [8s, 8s+8))
  *   v_cache  bf16 [num_pages][num_kv_heads][128 dims][16 token slots]
  * written by atf_kv_write_bf16 (RoPE applied to K there); page_table is int32
  * [batch][max_pages] of page ids.  Token slots of a page that were never written
@@ -39,9 +46,10 @@
 extern "C" {
 #endif
 
-#define ATF_ABI_VERSION 1
+#define ATF_ABI_VERSION 2
 #define ATF_HEAD_DIM 128
 #define ATF_LEVELS 8
+#define ATF_SLICES 16
 #define ATF_PAGE_SIZE 16
 #define ATF_LAYOUT_HALF_SPLIT 0
 #define ATF_LAYOUT_SORTED_PAIR 1
@@ -125,7 +133,8 @@ size_t atf_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, 
  * q/out are bf16 [batch][num_q_heads][128] with element strides (q: 16-byte
  * aligned, strides multiples of 8; out: 8-byte aligned, strides multiples of 4); seq_lens is a
  * device int32 [batch] whose entries must not exceed max_seq_len.  The window
- * is quantized per page (block_n = 16): page p reads its first L(p) levels only.
+ * is quantized per page (block_n = 16): page p reads its first L(p) levels only
+ * (2 L(p) slices of its K block).
  *
  * Replaces flashinfer.decode.single_decode_with_kv_cache_with_jit_module(...,
  * maybe_zhi_slice=...) of the FlashInfer window port
@@ -138,6 +147,29 @@ int atf_decode_paged_bf16(void* out, int64_t o_sb, int64_t o_sh,
                           int batch, int num_q_heads, int num_kv_heads, int max_seq_len,
                           const int32_t* zhi, float sm_scale, const float* rope_cs, int rope_max_pos,
                           int layout, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * atf_decode_paged_bf16 with the per-slice (vec8) window table of the
+ * FlashInfer port and its per-key rule: slice s of the key at position pos is
+ * read iff seq_len - 1 - pos <= zhi_slice[s] (kernels/flashinfer_port/
+ * decode.cuh.diff:47-89, gates/g2_correctness.py:37-70), with no minimum (a key
+ * past every slice scores 0).  zhi_slice is a HOST int32 [ATF_SLICES],
+ * non-negative and non-increasing, or NULL (window OFF).  Each page reads the
+ * slices of its youngest key; an older key's slices past its limit are masked.
+ * Same workspace as atf_decode_paged_bf16.
+ *
+ * Replaces single_decode_with_kv_cache_with_jit_module(mod, q, k, v, None,
+ * zhi_slice, ...) (kernels/flashinfer_port/fiwin_common.py:96-112), whose
+ * zhi_slice is fiwin_common.zhi_slice_vec8 (fiwin_common.py:35-47).
+ */
+int atf_decode_paged_slices_bf16(void* out, int64_t o_sb, int64_t o_sh,
+                                 const void* q, int64_t q_sb, int64_t q_sh,
+                                 const void* k_cache, const void* v_cache, int num_pages,
+                                 const int32_t* page_table, int max_pages, const int32_t* seq_lens,
+                                 int batch, int num_q_heads, int num_kv_heads, int max_seq_len,
+                                 const int32_t* zhi_slice, float sm_scale, const float* rope_cs,
+                                 int rope_max_pos, int layout, void* workspace, size_t workspace_bytes,
+                                 void* stream);
 
 /*
  * atf_decode_paged_bf16 for callers that cannot allocate device memory (code

@@ -80,6 +80,23 @@ def decode_oracle(q, k, v, base, k_ret, rope):
     return o[0, :, 0, :]
 
 
+def decode_oracle_vec8(q, k, v, base, zhi8, rope, layout="half_split"):
+    """Per-key vec8 decode oracle: q [Hq, D], k/v [N, Hkv, D] bf16 (half-split,
+    or sorted pair pre-rotated); query at position N-1; slice t of a key at age
+    a is read iff a <= zhi8[t] (ref_decode_sliced, slice width 8)."""
+    N = k.shape[0]
+    if rope:
+        kr = rotate(k.unsqueeze(0), torch.arange(N), base)[0]
+        qr = rotate(q.unsqueeze(0).unsqueeze(0), torch.tensor([N - 1]), base)[0, 0]
+    else:
+        kr, qr = k.float(), q.float()
+    if layout == "half_split":
+        kr, qr = OA.to_sorted(kr), OA.to_sorted(qr)
+    zt = [2 ** 31 - 1] * 16 if zhi8 is None else [int(z) for z in zhi8]
+    o, _ = OA.ref_decode_sliced(qr, kr, v.float(), zt, 8)
+    return o
+
+
 def errors(out, ref):
     d = (out.float().cpu() - ref.float().cpu()).abs()
     return d.max().item(), d.mean().item()

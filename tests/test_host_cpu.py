@@ -100,6 +100,26 @@ def test_decode_s_matches_tile_rule():
         assert s == read / (8 * -(-N // 16))
 
 
+def test_decode_s_slices_counts_the_pages_youngest_key():
+    """decode_s_slices (the vec8 decode's K bytes) counts, per 16-token page,
+    the slices of its youngest key, from the oracle's vec8 table; it sits
+    between the per-key theory (theory_s_vec8, which charges every key its own
+    slices) and the level table's page count."""
+    from atflash import atflash_window as AW, fiwin_common as FW
+    for base, k, N in [(1e7, 2.0, 131072), (1e4, 0.5, 3001), (1e4, 0.05, 5000)]:
+        z8 = WR.zhi_slice_vec8(128, base, k)
+        s, ceil = FW.decode_s_slices(N, z8, 16)
+        n_pages = -(-N // 16)
+        read = 0
+        for p in range(n_pages):
+            youngest = min(N - 1, 16 * p + 15)
+            read += sum(1 for t in range(16) if (N - 1) - youngest <= z8[t])
+        assert s == read / (16 * n_pages) and ceil == 2 / (1 + s)
+        theory, _ = WR.theory_s_vec8(128, base, k, N)
+        s_lv, _ = FW.decode_s(N, AW.window_zhi_from_kret(128, base, k, 1 << 20), 128, 16)
+        assert theory - 1e-12 <= s <= s_lv + 1e-12
+
+
 # ---------------------------------------------------------------- C ABI
 
 def _declared_symbols():
@@ -124,7 +144,9 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert hasattr(raw, name), name
     L = _lib.lib()
-    assert L.atf_abi_version() == 1
+    with open(HEADER) as f:
+        header_version = int(re.search(r"#define ATF_ABI_VERSION (\d+)", f.read()).group(1))
+    assert L.atf_abi_version() == header_version == _lib.ABI_VERSION
 
 
 def test_workspace_size_formula():
@@ -221,6 +243,35 @@ def test_noalloc_decode_validates_like_the_workspace_entry_point(no_gpu):
     assert L.atf_decode_paged_bf16_noalloc(*a.values()) == _lib.ATF_ERR_INVALID
 
 
+def test_slice_table_decode_validation(no_gpu):
+    """The per-slice (vec8) decode entry point: a table must be non-negative and
+    non-increasing (a page's slices must form a prefix); no cap rule applies
+    (a key past every slice scores 0, as in the FlashInfer port).  Valid
+    tables stop at the workspace check (the pointers are never used)."""
+    from atflash import fiwin_common as FW
+    _lib = _lib_or_skip()
+    L = _lib.lib()
+    a = dict(out=FAKE, o_sb=0, o_sh=0, q=FAKE, q_sb=0, q_sh=0, k=FAKE, v=FAKE, num_pages=256, table=FAKE,
+             max_pages=256, seq_lens=FAKE, batch=1, hq=28, hkv=4, max_seq_len=4096, zhi=None, scale=0.088,
+             rope=None, rope_max=0, layout=0, ws=FAKE, ws_bytes=0, stream=None)
+
+    def call(**kw):
+        b = dict(a)
+        b.update(kw)
+        return L.atf_decode_paged_slices_bf16(*b.values())
+    assert call() == _lib.ATF_ERR_WORKSPACE                                    # window OFF
+    good = (ctypes.c_int32 * 16)(*FW.zhi_slice_vec8(128, 1e4, 0.05).tolist())
+    assert good[0] < 4095                                                       # below the context: allowed
+    assert call(zhi=good) == _lib.ATF_ERR_WORKSPACE
+    up = (ctypes.c_int32 * 16)(*([100] * 15 + [200]))
+    assert call(zhi=up) == _lib.ATF_ERR_INVALID
+    assert b"non-increasing" in L.atf_last_error()
+    neg = (ctypes.c_int32 * 16)(*([100] * 15 + [-1]))
+    assert call(zhi=neg) == _lib.ATF_ERR_INVALID
+    assert call(hq=68) == _lib.ATF_ERR_UNSUPPORTED                              # GQA group 17
+    assert call(batch=0) == 0
+
+
 def test_table_cap_below_longest_distance_is_refused(no_gpu):
     """zhi[0] is the table's cap; a cap below the call's longest causal distance
     would drop levels the rule keeps (e2e_pipeline/atflash_e2e_fafi.py:55-58), so
@@ -255,6 +306,9 @@ def test_ops_refuse_cpu_tensors_and_bad_tables():
         interface._flash_attn_fwd(q, k, k, causal=False)
     with pytest.raises(ValueError, match="8 entries"):
         interface._zhi_list([1, 2, 3])
+    with pytest.raises(ValueError, match="8 or 16 entries"):
+        interface._zhi_list([1] * 12, interface._DECODE_TABLES)
+    assert interface._zhi_list([5] * 16, interface._DECODE_TABLES) == [5] * 16
     with pytest.raises(ValueError):
         _lib.zhi_array(list(range(7)))
     with pytest.raises(ValueError):

@@ -10,12 +10,13 @@ pytestmark = pytest.mark.gpu
 
 
 def _expected_pages(k, v, table, start, n_pages_pool, hkv, layout=0, init=None):
-    """CPU model of the cache layout for one sequence (no RoPE); `init` is the
+    """CPU model of the cache layout for one sequence (no RoPE): K as 16 slices of
+    8 dims in wavelength order, V transposed; `init` is the
     cache content before the write (zeros if None).  Tokens at negative
     positions are not written."""
     P = 64
     if init is None:
-        ek = torch.zeros((n_pages_pool, hkv, 8, 16, 16), dtype=torch.bfloat16)
+        ek = torch.zeros((n_pages_pool, hkv, 16, 16, 8), dtype=torch.bfloat16)
         ev = torch.zeros((n_pages_pool, hkv, 128, 16), dtype=torch.bfloat16)
     else:
         ek, ev = init[0].clone(), init[1].clone()
@@ -26,11 +27,13 @@ def _expected_pages(k, v, table, start, n_pages_pool, hkv, layout=0, init=None):
             continue
         pg = table[pos // 16]
         s = pos % 16
-        for lv in range(8):
-            c0 = P - 8 * (lv + 1) if layout == 0 else 16 * lv
-            c1 = c0 + P if layout == 0 else 16 * lv + 8
-            ek[pg, :, lv, s, :8] = k[t, :, c0:c0 + 8]
-            ek[pg, :, lv, s, 8:] = k[t, :, c1:c1 + 8]
+        for sl in range(16):
+            if layout == 0:  # half-split: pairs r in [P-4(sl+1), P-4sl), first halves then second halves
+                r0 = P - 4 * (sl + 1)
+                ek[pg, :, sl, s, :4] = k[t, :, r0:r0 + 4]
+                ek[pg, :, sl, s, 4:] = k[t, :, r0 + P:r0 + P + 4]
+            else:  # sorted pair: dims [8sl, 8sl+8)
+                ek[pg, :, sl, s, :] = k[t, :, 8 * sl:8 * sl + 8]
         ev[pg, :, :, slot_of[s]] = v[t]
     return ek, ev
 
@@ -45,7 +48,7 @@ def test_cache_layout_bit_exact(layout, hkv, dev):
     k = H.randn_bf16((n, hkv, H.D), g)
     v = H.randn_bf16((n, hkv, H.D), g)
     table = torch.randperm(pool, generator=g)[:-(-(start + n) // 16)].to(torch.int32)
-    kc = torch.zeros((pool, hkv, 8, 16, 16), dtype=torch.bfloat16, device=dev)
+    kc = torch.zeros((pool, hkv, 16, 16, 8), dtype=torch.bfloat16, device=dev)
     vc = torch.zeros((pool, hkv, 128, 16), dtype=torch.bfloat16, device=dev)
     torch.ops.atflash.kv_write(kc, vc, k[None].to(dev), v[None].to(dev),
                                torch.tensor([start], dtype=torch.int32, device=dev),
@@ -62,7 +65,7 @@ def test_rope_at_write_matches_fp32_rotation(dev):
     k = H.randn_bf16((n, hkv, H.D), g)
     v = H.randn_bf16((n, hkv, H.D), g)
     table = torch.arange(-(-n // 16), dtype=torch.int32)
-    kc = torch.zeros((len(table), hkv, 8, 16, 16), dtype=torch.bfloat16, device=dev)
+    kc = torch.zeros((len(table), hkv, 16, 16, 8), dtype=torch.bfloat16, device=dev)
     vc = torch.zeros((len(table), hkv, 128, 16), dtype=torch.bfloat16, device=dev)
     rt = R.rope_table(n, R.inv_freq(H.D, base, dev))
     torch.ops.atflash.kv_write(kc, vc, k[None].to(dev), v[None].to(dev),
@@ -81,7 +84,7 @@ def test_rope_at_write_matches_fp32_rotation(dev):
 
 
 def _random_cache(pool, hkv, g):
-    return (H.randn_bf16((pool, hkv, 8, 16, 16), g), H.randn_bf16((pool, hkv, 128, 16), g))
+    return (H.randn_bf16((pool, hkv, 16, 16, 8), g), H.randn_bf16((pool, hkv, 128, 16), g))
 
 
 def test_partial_pages_keep_the_other_slots(dev):

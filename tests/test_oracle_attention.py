@@ -168,6 +168,63 @@ def test_sliced_decode_equals_tile_rule_at_block_n_1():
     assert (got - ref).abs().max().item() < 1e-5
 
 
+def _sliced_decode_fp64(q, k, v, zhi, slice_w, shift=0):
+    """Brute force of the per-key slice rule in fp64, key by key and slice by
+    slice (gates/g2_correctness.py:37-70): slice t of the key at age
+    a = N-1-pos is summed iff a <= zhi[t] + shift (shift != 0 plants an
+    off-by-one in the boundary)."""
+    hq, d = q.shape
+    N, hkv, _ = k.shape
+    g = hq // hkv
+    out = torch.zeros((hq, d), dtype=torch.float64)
+    for h in range(hq):
+        s = torch.zeros(N, dtype=torch.float64)
+        for n in range(N):
+            age = N - 1 - n
+            for t in range(d // slice_w):
+                if age <= zhi[t] + shift:
+                    sl = slice(t * slice_w, (t + 1) * slice_w)
+                    s[n] += (q[h, sl].double() * k[n, h // g, sl].double()).sum()
+        p = torch.softmax(s / math.sqrt(d), dim=0)
+        out[h] = p @ v[:, h // g].double()
+    return out
+
+
+# a vec8 table with a boundary at every age from 0 up, some slices never read
+# (a key past every slice scores 0) and repeated entries
+VEC8_TABLE = [250, 250, 180, 120, 90, 60, 30, 10, 5, 3, 2, 1, 1, 0, 0, 0]
+
+
+def test_sliced_decode_vec8_equals_fp64_brute_force():
+    """8-dim slices (the FlashInfer port's vec8 table) against the key-by-key
+    fp64 brute force; a planted off-by-one at the slice boundary differs."""
+    N = 300
+    q, k, v = _rand((6, D), 40), _rand((N, 2, D), 41), _rand((N, 2, D), 42)
+    got, _ = OA.ref_decode_sliced(q, k, v, VEC8_TABLE, 8)
+    ref = _sliced_decode_fp64(q, k, v, VEC8_TABLE, 8)
+    assert (got.double() - ref).abs().max().item() < 1e-5
+    planted = _sliced_decode_fp64(q, k, v, VEC8_TABLE, 8, shift=-1)
+    assert (got.double() - planted).abs().max().item() > 1e-3
+
+
+def test_sliced_decode_vec8_with_paired_entries_equals_width_16():
+    """A vec8 table holding each level's entry on its two slices gives the
+    16-dim slice result.  From the same widths, the vec8 table reads slice 2l
+    exactly where the level table reads level l (both floor(w[8l]) below the
+    cap) and slice 2l+1 no further: the finer table reads a subset."""
+    N = 400
+    zhi16 = WR.zhi_table(WR.wavelengths_sorted(D, 1e4, 0.05), D, N)
+    zhi8 = [zhi16[t // 2] for t in range(16)]
+    q, k, v = _rand((4, D), 43), _rand((N, 1, D), 44), _rand((N, 1, D), 45)
+    a, _ = OA.ref_decode_sliced(q, k, v, zhi8, 8)
+    b, _ = OA.ref_decode_sliced(q, k, v, zhi16, 16)
+    assert (a - b).abs().max().item() < 1e-6
+    z8 = WR.zhi_slice_vec8(D, 1e4, 0.05)
+    trimmed = [lv for lv in range(1, 8) if zhi16[lv] < N - 1]
+    assert trimmed
+    assert all(z8[2 * lv] == zhi16[lv] and z8[2 * lv + 1] <= z8[2 * lv] for lv in trimmed)
+
+
 def test_lse_merge_equals_unsplit():
     s = _rand((3, 200), 31) * 3
     vv = _rand((200, D), 32)
