@@ -5,7 +5,8 @@ attention function registered with transformers' AttentionInterface under a
 name without "flash" in it (transformers v5 routes such names to its own
 FlashAttention path, e2e:127-130), dispatching on the query length:
 
-* L == 1  -> windowed split-KV decode;
+* L == 1  -> windowed split-KV decode with the FlashInfer port's per-slice
+             (vec8) table and per-key rule, as the reference decodes (e2e:104-110);
 * L > 1   -> windowed causal prefill, bottom-right aligned when L < S
              (a continued/chunked prefill).
 
@@ -26,7 +27,7 @@ window table (plain causal attention).
 
 Where the K/V live.  The reference's decode reads the HF cache in place (HND
 view of the DynamicCache tensors, e2e:100-110).  The kernels here read a paged,
-level-blocked cache instead, so the serving path is `PagedCache`: an HF `Cache`
+slice-blocked cache instead, so the serving path is `PagedCache`: an HF `Cache`
 whose per-layer `update` appends the new keys and values to that layer's pages
 with the cache-writer kernel (rotating K there with rope_at_load) and returns
 the chunk itself.  The hook recognises a layer of a bound PagedCache by
@@ -253,7 +254,7 @@ class WindowAttention:
             if (owner.rope_cs is not None) != self.rope_at_load:
                 raise ValueError("the cache was made for the other RoPE mode of this hook")
             if L == 1:
-                zhi = list(self.window.decode_zhi) if windowed else None
+                zhi = list(self.window.decode_zhi8) if windowed else None
                 o = ops.decode_paged(query[:, :, 0, :], lyr.k, lyr.v, owner.page_table, owner.seq_lens(S), S, zhi,
                                      scale, owner.rope_cs, _lib.LAYOUT_HALF_SPLIT)
                 return o.view(b, 1, hq, d), None
@@ -266,7 +267,7 @@ class WindowAttention:
         if L == 1:
             kc, vc, table = I.pack_kv(key.transpose(1, 2), value.transpose(1, 2), rope=rt)
             seq = torch.full((b,), S, dtype=torch.int32, device=query.device)
-            zhi = list(self.window.decode_zhi) if windowed else None
+            zhi = list(self.window.decode_zhi8) if windowed else None
             o = ops.decode_paged(query[:, :, 0, :], kc, vc, table, seq, S, zhi, scale, rt, 0)
             return o.view(b, 1, hq, d), None
         zhi = self.window.prefill_zhi if windowed else None

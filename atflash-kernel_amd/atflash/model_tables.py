@@ -26,6 +26,7 @@ from dataclasses import dataclass
 import torch
 
 from . import atflash_window as AW
+from . import fiwin_common as FW
 
 # model_type -> (module under transformers.models, rotary class)
 _ROTARY = {
@@ -89,7 +90,8 @@ class ModelWindow:
     k_decode: float
     n_ctx: int
     prefill_zhi: tuple      # level table for prefill (16-dim levels)
-    decode_zhi: tuple       # level table for decode
+    decode_zhi: tuple       # level table for decode (page rule)
+    decode_zhi8: tuple      # per-slice (vec8) table for decode, per-key rule
     sm_scale: float         # head_dim ** -0.5
     inv_freq: torch.Tensor  # real inverse frequencies, fp32 [P]
     attention_scaling: float
@@ -125,6 +127,9 @@ def window_from_config(config, k_prefill: float = 2.0, k_decode: float = 2.0, n_
               max(WIN_ZHI_CAP, int(getattr(config, "max_position_embeddings", 0) or 0)))
     fz = tuple(AW.window_zhi_from_kret(d, base, float(k_prefill), cap))
     dz = tuple(AW.window_zhi_from_kret(d, base, float(k_decode), cap))
+    # decode as the reference's harness does it: the FlashInfer port's vec8
+    # table at the decode k (e2e_pipeline/atflash_e2e_fafi.py:168-171)
+    dz8 = tuple(int(x) for x in FW.zhi_slice_vec8(d, base, float(k_decode)).tolist())
     return ModelWindow(head_dim=d, raw_base=base, k_prefill=float(k_prefill), k_decode=float(k_decode), n_ctx=cap,
-                       prefill_zhi=fz, decode_zhi=dz, sm_scale=d ** -0.5, inv_freq=inv,
+                       prefill_zhi=fz, decode_zhi=dz, decode_zhi8=dz8, sm_scale=d ** -0.5, inv_freq=inv,
                        attention_scaling=attn_scale)

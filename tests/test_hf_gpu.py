@@ -45,8 +45,11 @@ def _oracle_attention(module, query, key, value, attention_mask, scaling=None, d
     qs, ks = OA.to_sorted(query.float().cpu()), OA.to_sorted(key.float().cpu())
     vv = value.float().cpu()
     w = WR.wavelengths_sorted(d, BASE, K_RET)
-    if L == 1:
-        out = OA.ref_window_attn(qs, ks, vv, w, phase="decode", block_m=1, block_n=16)
+    if L == 1:  # the hook decodes with the vec8 table, per-key rule (gates/g2_correctness.py:37-70)
+        z8 = WR.zhi_slice_vec8(d, BASE, K_RET)
+        hkv = ks.shape[1]
+        out = torch.stack([OA.ref_decode_sliced(qs[bi, :, 0], ks[bi].transpose(0, 1), vv[bi].transpose(0, 1), z8, 8)[0]
+                           for bi in range(b)])[:, :, None, :]
     else:
         out = OA.ref_window_attn(qs, ks, vv, w, phase="prefill", block_m=32, block_n=32, q_offset=S - L)
     return out.transpose(1, 2).contiguous().to(query.dtype).to(query.device), None

@@ -16,6 +16,7 @@ from transformers import LlamaConfig, Qwen2Config  # noqa: E402
 
 from atflash import atflash_window as AW  # noqa: E402
 from atflash import model_tables as MT  # noqa: E402
+from oracle import window_rule as WR  # noqa: E402
 
 
 def qwen05b():
@@ -79,7 +80,19 @@ def test_tables_use_the_raw_base_and_equal_recorded_ones(golden):
         win = MT.window_from_config(cfg, 2.0, 64.0, n_ctx=1100000)
         assert win.prefill_zhi == tuple(AW.window_zhi_from_kret(128, 1e7, 2.0, 1100000))
         assert win.decode_zhi == tuple(AW.window_zhi_from_kret(128, 1e7, 64.0, 1100000))
+        assert win.decode_zhi8 == tuple(WR.zhi_slice_vec8(128, 1e7, 64.0))
         assert win.sm_scale == 128 ** -0.5 and win.head_dim == 128
+    # the decode's vec8 table equals the one the reference's harness recorded
+    # (fi_zhi8 of the run summaries) for the same base and decode k
+    seen = 0
+    for r in golden["summaries"]:
+        if not r.get("fi_zhi8"):
+            continue
+        cfg = {5e5: llama32_3b, 1e7: qwen7b1m}[r["raw_base"]]()
+        win = MT.window_from_config(cfg, r["k_prefill"], r["k_decode"], n_ctx=1100000)
+        assert list(win.decode_zhi8) == r["fi_zhi8"]
+        seen += 1
+    assert seen >= 10
     llama = [r for r in golden["summaries"] if r.get("fa_zhi") and r["raw_base"] == 5e5 and r["k_prefill"] == 2.0]
     assert llama, "no recorded Llama (base 5e5) table"
     for rec in llama:
