@@ -11,8 +11,9 @@ decode   `single_decode_with_kv_cache(q, k, v, maybe_zhi=...)` as the FlashInfer
 paged    `prefill_paged` / `decode_paged` on a PagedKVCache, the serving path.
 
 Differences from the reference that a caller sees:
-  * the window table is the 16-dim level table zhi for both prefill and decode
-    (decode quantizes it per 16-token page, block_n = 16);
+  * prefill takes the 16-dim level table zhi; decode takes either the
+    FlashInfer port's per-slice vec8 table (16 entries, per-key rule) or the
+    level table (8 entries, quantized per 16-token page, block_n = 16);
   * inputs may stay in the half-split (HF rotate_half) layout and RoPE can be
     fused (`rope=` a table from atflash.rope.rope_table); the reference's
     wavelength-sorted layout is accepted with layout="sorted_pair" and rope=None.
