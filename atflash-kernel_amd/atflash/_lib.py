@@ -100,15 +100,25 @@ def check(code):
     raise AtflashError(code, msg)
 
 
+_ZHI_ARRAYS = {}
+
+
 def zhi_array(zhi, n=LEVELS):
     """Host int32[n] for a window table (n = LEVELS: the level table; n =
-    SLICES: the per-slice vec8 table), or None (window OFF)."""
+    SLICES: the per-slice vec8 table), or None (window OFF).  The arrays are
+    kept per table (the library copies the values at each call), so a decode
+    loop does not rebuild one per call."""
     if zhi is None:
         return None
-    vals = [int(x) for x in (zhi.tolist() if isinstance(zhi, torch.Tensor) else zhi)]
+    vals = tuple(int(x) for x in (zhi.tolist() if isinstance(zhi, torch.Tensor) else zhi))
     if len(vals) != n:
         raise ValueError(f"window table must have {n} entries (head_dim / {HEAD_DIM // n}), got {len(vals)}")
-    return (ctypes.c_int32 * n)(*vals)
+    arr = _ZHI_ARRAYS.get(vals)
+    if arr is None:
+        if len(_ZHI_ARRAYS) >= 256:
+            _ZHI_ARRAYS.clear()
+        arr = _ZHI_ARRAYS[vals] = (ctypes.c_int32 * n)(*vals)
+    return arr
 
 
 K_BLOCK_SHAPE = (SLICES, PAGE_SIZE, SLICE_DIMS)  # one (page, kv head) K block of the cache

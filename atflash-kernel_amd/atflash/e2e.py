@@ -14,8 +14,10 @@ clock around the whole request.  The model is the Qwen2.5-7B architecture
 RMSNorm, RoPE base 1e7) with random weights (HF's initializer, std 0.02, seeded)
 in bf16 -- no checkpoint is loaded -- and the prompt is uniform-random token
 ids from a seeded generator.  OFF runs the same kernels with no window table;
-k2 / k64 use the level tables of k = 2 / 64 for prefill and decode alike, built
-from the model config with the reference's 1.1M cap.
+k2 / k64 use k = 2 / 64 for prefill and decode alike, built from the model
+config with the reference's 1.1M cap: the level table for prefill and the
+per-slice vec8 table (per-key rule) for decode, as the reference's harness
+(fa_zhi and fi_zhi8, e2e_pipeline/atflash_e2e_fafi.py:167-171).
 
 The C0 mode is gates/c0_chunk_neutrality.py:22-61: the prompt in one forward
 against the prompt in chunks, comparing the last logits and layer 0's cached

@@ -9,6 +9,11 @@
 Each op checks shapes and dtypes, then calls the HIP library on the current
 stream of the tensors' device.  There is no CPU or PyTorch fallback: a CPU
 tensor or a missing library is an error.
+
+The module-level functions `kv_write`, `prefill` and `decode_paged` are the
+same operations called directly from Python, without the dispatcher (whose
+per-call cost, about 20 us, would exceed a short decode's GPU time); the
+package's own entry points use them.
 """
 from typing import List, Optional, Tuple
 
@@ -50,7 +55,6 @@ def _rope(rope_cs):
     return rope_cs, rope_cs.shape[0]
 
 
-@torch.library.custom_op("atflash::kv_write", mutates_args=("k_cache", "v_cache"))
 def kv_write(k_cache: torch.Tensor, v_cache: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
              start_pos: torch.Tensor, page_table: torch.Tensor, rope_cs: Optional[torch.Tensor],
              layout: int) -> None:
@@ -76,12 +80,14 @@ def kv_write(k_cache: torch.Tensor, v_cache: torch.Tensor, k: torch.Tensor, v: t
         _lib.ptr(rope_cs), max_pos, _layout(layout), _lib.stream_of(k.device)))
 
 
-@kv_write.register_fake
+_kv_write_op = torch.library.custom_op("atflash::kv_write", kv_write, mutates_args=("k_cache", "v_cache"))
+
+
+@_kv_write_op.register_fake
 def _(k_cache, v_cache, k, v, start_pos, page_table, rope_cs, layout):
     return None
 
 
-@torch.library.custom_op("atflash::prefill", mutates_args=())
 def prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, page_table: torch.Tensor,
             nk: int, q_offset: int, zhi: Optional[List[int]], sm_scale: float,
             rope_cs: Optional[torch.Tensor], layout: int) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -109,7 +115,10 @@ def prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, page_
     return out, lse
 
 
-@prefill.register_fake
+_prefill_op = torch.library.custom_op("atflash::prefill", prefill, mutates_args=())
+
+
+@_prefill_op.register_fake
 def _(q, k_cache, v_cache, page_table, nk, q_offset, zhi, sm_scale, rope_cs, layout):
     B, Nq, Hq, D = q.shape
     return q.new_empty((B, Nq, Hq, D)), q.new_empty((B, Hq, Nq), dtype=torch.float32)
@@ -121,9 +130,8 @@ def _(q, k_cache, v_cache, page_table, nk, q_offset, zhi, sm_scale, rope_cs, lay
 _DECODE_WS = {}
 
 
-def _decode_workspace(device, nbytes):
-    stream = torch.cuda.current_stream(device)
-    key = (device.index, stream.cuda_stream)
+def _decode_workspace(device, handle, nbytes):
+    key = (device.index, handle)
     ws = _DECODE_WS.get(key)
     if ws is None or ws.numel() * 4 < nbytes:
         ws = torch.empty((max(nbytes, 16) + 3) // 4, dtype=torch.float32, device=device)
@@ -131,7 +139,6 @@ def _decode_workspace(device, nbytes):
     return ws
 
 
-@torch.library.custom_op("atflash::decode_paged", mutates_args=())
 def decode_paged(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, page_table: torch.Tensor,
                  seq_lens: torch.Tensor, max_seq_len: int, zhi: Optional[List[int]], sm_scale: float,
                  rope_cs: Optional[torch.Tensor], layout: int) -> torch.Tensor:
@@ -152,7 +159,8 @@ def decode_paged(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
     rope_cs, max_pos = _rope(rope_cs)
     L = _lib.lib()
     nbytes = int(L.atf_decode_workspace_bytes(B, Hq, hkv, int(max_seq_len)))
-    ws = _decode_workspace(q.device, nbytes)
+    stream = _lib.stream_of(q.device)
+    ws = _decode_workspace(q.device, stream.value, nbytes)
     out = torch.empty((B, Hq, _lib.HEAD_DIM), dtype=torch.bfloat16, device=q.device)
     slices = zhi is not None and len(zhi) == _lib.SLICES
     entry = L.atf_decode_paged_slices_bf16 if slices else L.atf_decode_paged_bf16
@@ -161,11 +169,14 @@ def decode_paged(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
         _lib.ptr(out), out.stride(0), out.stride(1), _lib.ptr(q), q.stride(0), q.stride(1),
         _lib.ptr(k_cache), _lib.ptr(v_cache), k_cache.shape[0], _lib.ptr(page_table), page_table.shape[1],
         _lib.ptr(seq_lens.contiguous()), B, Hq, hkv, int(max_seq_len), table, float(sm_scale),
-        _lib.ptr(rope_cs), max_pos, _layout(layout), _lib.ptr(ws), ws.numel() * 4, _lib.stream_of(q.device)))
+        _lib.ptr(rope_cs), max_pos, _layout(layout), _lib.ptr(ws), ws.numel() * 4, stream))
     return out
 
 
-@decode_paged.register_fake
+_decode_paged_op = torch.library.custom_op("atflash::decode_paged", decode_paged, mutates_args=())
+
+
+@_decode_paged_op.register_fake
 def _(q, k_cache, v_cache, page_table, seq_lens, max_seq_len, zhi, sm_scale, rope_cs, layout):
     return q.new_empty(q.shape)
 

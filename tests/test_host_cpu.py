@@ -314,3 +314,29 @@ def test_ops_refuse_cpu_tensors_and_bad_tables():
     with pytest.raises(ValueError):
         interface._layout_id("interleaved")
     assert ops._DECODE_WS == {}
+
+
+def test_registered_ops_and_direct_functions_agree():
+    """torch.ops.atflash.* (through the dispatcher) and the module functions
+    the package calls directly are the same operations: both are registered
+    or defined, take the same arguments and refuse CPU tensors alike."""
+    from atflash import _lib, ops
+    kc = torch.zeros((2, 1, *_lib.K_BLOCK_SHAPE), dtype=torch.bfloat16)
+    vc = torch.zeros((2, 1, 128, 16), dtype=torch.bfloat16)
+    q = torch.zeros((1, 4, 128), dtype=torch.bfloat16)
+    table = torch.zeros((1, 2), dtype=torch.int32)
+    seq = torch.full((1,), 20, dtype=torch.int32)
+    for fn in (ops.decode_paged, torch.ops.atflash.decode_paged):
+        with pytest.raises(ValueError, match="GPU"):
+            fn(q, kc, vc, table, seq, 20, [5] * 16, 0.1, None, 0)
+    qp = torch.zeros((1, 32, 4, 128), dtype=torch.bfloat16)
+    for fn in (ops.prefill, torch.ops.atflash.prefill):
+        with pytest.raises(ValueError, match="GPU"):
+            fn(qp, kc, vc, table, 32, 0, None, 0.1, None, 0)
+    kv = torch.zeros((1, 32, 1, 128), dtype=torch.bfloat16)
+    for fn in (ops.kv_write, torch.ops.atflash.kv_write):
+        with pytest.raises(ValueError, match="GPU"):
+            fn(kc, vc, kv, kv, torch.zeros(1, dtype=torch.int32), table, None, 0)
+    # the window table arrays are built once per table and reused
+    assert _lib.zhi_array([7] * 16, _lib.SLICES) is _lib.zhi_array(tuple([7] * 16), _lib.SLICES)
+    assert list(_lib.zhi_array([9] * 8)) == [9] * 8
