@@ -68,6 +68,10 @@ __device__ __forceinline__ int levels_of(const LevelTable& t, int z) {
   return n < 1 ? 1 : n;
 }
 
+// Word 3 of a raw buffer resource (no format conversion, 32-bit data format
+// field), as the raw buffer-load path of gfx9-family targets expects.
+constexpr int kBufferWord3 = 0x00020000;
+
 // The per-slice distance table of the decode kernel (kernel argument, SGPRs).
 struct SliceTable {
   int32_t zhi[kSlices];

@@ -36,10 +36,6 @@
 
 namespace atf {
 
-// Word 3 of a raw buffer resource (no format conversion, 32-bit data format
-// field), as the raw buffer-load path of gfx9-family targets expects.
-constexpr int kBufferWord3 = 0x00020000;
-
 // max / sum over the 4 lanes {l, l^16, l^32, l^48} that hold one query head.
 __device__ __forceinline__ float quad_max(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);

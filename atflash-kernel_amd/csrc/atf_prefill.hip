@@ -149,82 +149,67 @@ __device__ __forceinline__ int v_lds_elem(int d, int s) {
 // stricter when copies it does not count are in flight.  M0 holds the LDS
 // address for the copies (one wait state after it is written) and is restored.
 //
-// lds_copy_rows<N> copies N consecutive 1 KB rows: lane l reads 16 bytes at
-// base + voff(l) + 1024 i (a wave-uniform base in scalar registers plus a
-// per-lane offset) and writes LDS dst + 16 l + 1024 i.  The instruction's
-// immediate offset moves the global and the LDS address alike, so one M0
-// setting serves all N rows.
-template <int N>
-__device__ __forceinline__ void lds_copy_rows(const uint8_t* base, uint32_t voff, lds_u8* dst) {
-  static_assert(N >= 1 && N <= 4, "1 to 4 rows");
+// lds_copy_page copies the first `nbytes` (a multiple of 1 KB, at most 4 KB)
+// of a page through a raw buffer resource whose range is nbytes: it always
+// issues the four row loads, and the hardware range check turns the rows
+// past the range into zeros without a memory request.  Lane l reads 16 bytes
+// at base + voff(l) + 1024 i and writes LDS dst + 16 l + 1024 i (the
+// instruction's immediate offset moves the memory and the LDS address alike,
+// so one M0 setting serves all four rows).  One straight-line sequence serves
+// every row count: a switch over the count cost about 400 cycles of branching
+// per copying step, on the wave whose softmax sets the step when the window
+// trims the QK work.
+__device__ __forceinline__ void lds_copy_page(const uint8_t* base, uint32_t nbytes, uint32_t voff, lds_u8* dst) {
   const uint32_t la = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst)));
+  const uint64_t ad = reinterpret_cast<uint64_t>(base);
+  u32x4 rs;  // raw buffer resource: base, stride 0, num_records = nbytes
+  rs[0] = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(ad)));
+  rs[1] = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(ad >> 32))) & 0xffffu;
+  rs[2] = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(nbytes));
+  rs[3] = static_cast<uint32_t>(kBufferWord3);
   uint32_t saved;
-#define ATF_LDS_ROW(off) "global_load_lds_dwordx4 %1, %2 offset:" #off "\n\t"
-  if constexpr (N == 1)
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t" ATF_LDS_ROW(0) "s_mov_b32 m0, %0"
-                 : "=&s"(saved) : "v"(voff), "s"(base), "s"(la) : "memory");
-  else if constexpr (N == 2)
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t" ATF_LDS_ROW(0) ATF_LDS_ROW(1024)
-                 "s_mov_b32 m0, %0"
-                 : "=&s"(saved) : "v"(voff), "s"(base), "s"(la) : "memory");
-  else if constexpr (N == 3)
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t" ATF_LDS_ROW(0) ATF_LDS_ROW(1024)
-                 ATF_LDS_ROW(2048) "s_mov_b32 m0, %0"
-                 : "=&s"(saved) : "v"(voff), "s"(base), "s"(la) : "memory");
-  else
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t" ATF_LDS_ROW(0) ATF_LDS_ROW(1024)
-                 ATF_LDS_ROW(2048) ATF_LDS_ROW(3072) "s_mov_b32 m0, %0"
-                 : "=&s"(saved) : "v"(voff), "s"(base), "s"(la) : "memory");
-#undef ATF_LDS_ROW
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+               "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
+               "buffer_load_dwordx4 %1, %2, 0 offen offset:1024 lds\n\t"
+               "buffer_load_dwordx4 %1, %2, 0 offen offset:2048 lds\n\t"
+               "buffer_load_dwordx4 %1, %2, 0 offen offset:3072 lds\n\t"
+               "s_mov_b32 m0, %0"
+               : "=&s"(saved) : "v"(voff), "s"(rs), "s"(la) : "memory");
+}
+
+__device__ __forceinline__ void zero_page(lds_u8* dst, int lane) {
+  const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(dst + i * 1024 + lane * 16) = z;
 }
 
 // Stage one 4 KB page into LDS at `dst`: K (whole 1 KB level pairs covering
-// the first L levels) or V.  `pg` is the page id (-1: missing page,
-// zero-filled); `voff` is the lane's chunk offset within a copied 1 KB row
-// (k_copy_src or v_copy_src).
+// the first L levels; an odd L also copies level L, which is not read) or V.
+// `pg` is the page id (-1: missing page, zero-filled); `voff` is the lane's
+// chunk offset within a copied 1 KB row (k_copy_src or v_copy_src).
 __device__ __forceinline__ void pf_load_page(const PrefillArgs& a, int kvh, int pg, int L, bool is_v, lds_u8* dst,
                                              int lane, uint32_t voff) {
   if (pg < 0) {
-    const u32x4 z = {0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(dst + i * 1024 + lane * 16) = z;
+    zero_page(dst, lane);
     return;
   }
   const size_t blk = (static_cast<size_t>(pg) * a.hkv + kvh) * 4096;
-  if (is_v) {
-    lds_copy_rows<4>(reinterpret_cast<const uint8_t*>(a.v_cache) + blk, voff, dst);
-  } else {
-    // whole 1 KB level pairs (an odd L also copies level L, which is not read)
-    const uint8_t* src = reinterpret_cast<const uint8_t*>(a.k_cache) + blk;
-    switch ((L + 1) >> 1) {
-      case 4: lds_copy_rows<4>(src, voff, dst); break;
-      case 3: lds_copy_rows<3>(src, voff, dst); break;
-      case 2: lds_copy_rows<2>(src, voff, dst); break;
-      default: lds_copy_rows<1>(src, voff, dst); break;
-    }
-  }
+  const uint8_t* src = reinterpret_cast<const uint8_t*>(is_v ? a.v_cache : a.k_cache) + blk;
+  lds_copy_page(src, is_v ? 4096u : static_cast<uint32_t>((L + 1) >> 1) * 1024u, voff, dst);
 }
 
 // pf_load_page for the tile loop: the page's source is cbase + pg * pstride,
 // with the cache base (offset to the kv head) and the page stride computed once
-// before the loop, so the copy does not reload kernel arguments.
+// before the loop, so the copy does not reload kernel arguments; `rows` 1 KB
+// rows are copied.
 __device__ __forceinline__ void stage_page(const uint8_t* cbase, uint32_t pstride, int pg, int rows, lds_u8* dst,
                                            int lane, uint32_t voff) {
   if (pg < 0) {
-    const u32x4 z = {0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(dst + i * 1024 + lane * 16) = z;
+    zero_page(dst, lane);
     return;
   }
-  const uint8_t* src = cbase + static_cast<size_t>(static_cast<uint32_t>(pg)) * pstride;
-  switch (rows) {
-    case 4: lds_copy_rows<4>(src, voff, dst); break;
-    case 3: lds_copy_rows<3>(src, voff, dst); break;
-    case 2: lds_copy_rows<2>(src, voff, dst); break;
-    default: lds_copy_rows<1>(src, voff, dst); break;
-  }
+  lds_copy_page(cbase + static_cast<size_t>(static_cast<uint32_t>(pg)) * pstride, static_cast<uint32_t>(rows) * 1024u,
+                voff, dst);
 }
 
 // S^T (32 keys x 32 rows) of one 32-key block over its first L levels: one MFMA
