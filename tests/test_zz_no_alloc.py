@@ -66,3 +66,41 @@ def test_noalloc_decode_equals_workspace_decode(dev):
     k, v = [t.cpu() for t in H.gpu_qkv(1, 777, 1, 4, dev, seed=71 + 2, nq=1)[1:]]
     ref = H.decode_oracle(big["q"][2].cpu(), k[0], v[0], 1e7, 2.0, True)
     H.assert_close(a[2], ref, "noalloc, 777 tokens")
+
+
+def test_noalloc_decode_replays_in_a_hip_graph(dev):
+    """The caller the entry point is for: a decode captured once into a HIP
+    graph (torch.cuda.graph) and replayed with new query values written into
+    the same input buffer, eager work and synchronisations between replays.
+    Every replay equals the eager call on the same inputs, bit for bit."""
+    from atflash import _lib
+    print("[noalloc] graph: B=2 Qwen shape, 5000/1200 tokens, k=2, RoPE at load", flush=True)
+    c = _case([5000, 1200], 28, 4, 1e7, 2.0, True, dev, seed=81)
+    q1 = c["q"].clone()
+    q2 = H.gpu_qkv(2, 1, 28, 1, dev, seed=181, nq=1)[0][:, 0].contiguous()
+    eager1 = _decode(c, noalloc=True)  # also looks the scratch address up outside the capture
+    c["q"].copy_(q2)
+    eager2 = _decode(c, noalloc=True)
+    c["q"].copy_(q1)
+    torch.cuda.synchronize()
+
+    L = _lib.lib()
+    B, maxlen = 2, 5000
+    out = torch.empty((B, 28, H.D), dtype=torch.bfloat16, device=dev)
+    rt = c["rt"]
+    zhi = _lib.zhi_array(c["zhi"])
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = L.atf_decode_paged_bf16_noalloc(
+            _lib.ptr(out), out.stride(0), out.stride(1), _lib.ptr(c["q"]), c["q"].stride(0), c["q"].stride(1),
+            _lib.ptr(c["cache"].k), _lib.ptr(c["cache"].v), c["cache"].num_pages, _lib.ptr(c["table"]),
+            c["table"].shape[1], _lib.ptr(c["seq"]), B, 28, 4, maxlen, zhi, H.D ** -0.5, _lib.ptr(rt),
+            rt.shape[0], 0, _lib.stream_of(out.device))
+    _lib.check(rc)
+    for i, (qv, want) in enumerate([(q1, eager1), (q2, eager2), (q1, eager1)]):
+        c["q"].copy_(qv)
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.cpu(), want), f"replay {i}"
