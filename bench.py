@@ -400,7 +400,8 @@ def main():
                          "used to calibrate the FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path (see DESIGN.md, sharding).",
+        print("bench.py measures one GPU only: this build has no multi-GPU path; a larger job would shard the "
+              "kv heads and the key range across GPUs and merge the partials by log-sum-exp.",
               file=sys.stderr)
         sys.exit(2)
     import torch
