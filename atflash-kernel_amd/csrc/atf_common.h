@@ -72,6 +72,11 @@ __device__ __forceinline__ int levels_of(const LevelTable& t, int z) {
 // field), as the raw buffer-load path of gfx9-family targets expects.
 constexpr int kBufferWord3 = 0x00020000;
 
+// Cache-policy operand of a buffer load that streams data read once: the
+// non-temporal bit (`nt`).  On a decode-shaped probe (4 KB blocks in random
+// order, 268 MB per call) it raises the read rate from 5.8 to 6.6 TB/s.
+constexpr int kLoadStream = 2;
+
 // The per-slice distance table of the decode kernel (kernel argument, SGPRs).
 struct SliceTable {
   int32_t zhi[kSlices];

@@ -133,7 +133,8 @@ __device__ __forceinline__ void dec_load_page(const DecodeArgs& a, int h, int ra
   // in-window slices and yields zeros for the others; an invalid page entry
   // gets an empty range.  The loads are therefore unconditional: wave-uniform
   // base, 32-bit lane offset, immediate row offset, no per-load address
-  // arithmetic.
+  // arithmetic.  Every page is read once per call, so the loads are
+  // non-temporal.
   const size_t blk_bytes = (static_cast<size_t>(ok ? pg : 0) * a.hkv + h) * (kBlockElems * 2);
   const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(a.k_cache) + blk_bytes / 2, 0, ok ? ns * (kPage * kSliceDims * 2) : 0, kBufferWord3);
@@ -143,14 +144,14 @@ __device__ __forceinline__ void dec_load_page(const DecodeArgs& a, int h, int ra
   const uint32_t koff = static_cast<uint32_t>(lane) << 4;
 #pragma unroll
   for (int lp = 0; lp < 4; ++lp)
-    r.k[lp] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, koff + lp * 1024u, 0, 0));
+    r.k[lp] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, koff + lp * 1024u, 0, kLoadStream));
   // V^T operand: d row 16*db + lane%16, tokens 4*(lane/16)..+3 -> stored slots.
   const int grp = lane >> 4;
   const int slot0 = 4 * ((grp == 1) ? 2 : (grp == 2 ? 1 : grp));
   const uint32_t voff = (static_cast<uint32_t>(lane & 15) << 5) + static_cast<uint32_t>(slot0) * 2u;
 #pragma unroll
   for (int db = 0; db < 8; ++db)
-    r.v[db] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rv, voff + db * 512u, 0, 0));
+    r.v[db] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rv, voff + db * 512u, 0, kLoadStream));
 }
 
 // two waves per SIMD: at most 256 registers per wave
