@@ -57,23 +57,16 @@ struct PageRegs {
   bool mask;   // per-key rule with a slice boundary inside the page
 };
 
-// Page-table entries of the kDecUnroll pages starting at p0, in vector
-// registers (every lane holds the same value), -1 for pages at or past p_end.
-// The loads are unconditional (the index is clamped into [p_begin, p_end)) and
-// the past-the-end entries are selected afterwards: a load guarded by a branch
-// with a default value makes the compiler wait for every outstanding load
-// before the register's next use.  A wave fetches the entries of its next
-// group while it computes the current one, so the K/V loads of a group are
-// issued back to back without waiting for the table.
-__device__ __forceinline__ void dec_fetch_group(const DecodeArgs& a, int b, int p0, int p_begin, int p_end,
-                                                int (&e)[kDecUnroll]) {
+// Page-table entry of page p (a vector register; every lane holds the same
+// value).  The load is unconditional, its index clamped into [p_begin, p_end):
+// an entry for a page past the split is fetched but never used (its page is
+// not loaded).  A load guarded by a branch with a default value would make the
+// compiler wait for every outstanding load before the register's next use.
+// A wave fetches a page's entry one stride ahead of its use, so the page loads
+// are issued without waiting for the table.
+__device__ __forceinline__ int dec_fetch_entry(const DecodeArgs& a, int b, int p, int p_begin, int p_end) {
   const int* row = a.page_table + static_cast<int64_t>(b) * a.max_pages;
-#pragma unroll
-  for (int u = 0; u < kDecUnroll; ++u) {
-    const int p = p0 + u;
-    const int v = row[max(p_begin, min(p, p_end - 1))];
-    e[u] = (p < p_end) ? v : -1;
-  }
+  return row[max(p_begin, min(p, p_end - 1))];
 }
 
 // Slice count of a key at a fixed offset in its page as the page index p walks
@@ -120,13 +113,13 @@ __device__ __forceinline__ void page_slices(const DecodeArgs& a, SliceWalker& yo
 }
 
 // K and V operands of page p whose page-table entry is `raw`, reading its first
-// ns slices of K.
-__device__ __forceinline__ void dec_load_page(const DecodeArgs& a, int h, int raw, int p, int ns, bool mask, int lane,
-                                              PageRegs& r) {
+// ns slices of K; a page outside the split (in_split false) reads nothing.
+__device__ __forceinline__ void dec_load_page(const DecodeArgs& a, int h, int raw, bool in_split, int p, int ns,
+                                              bool mask, int lane, PageRegs& r) {
   r.n0 = p * kPage;
   r.mask = mask;
   const int pg = __builtin_amdgcn_readfirstlane(raw);
-  const bool ok = pg >= 0 && pg < a.num_pages;
+  const bool ok = in_split && pg >= 0 && pg < a.num_pages;
   // The page's K and V blocks as range-checked buffer resources: a load at or
   // past the range returns zeros without a memory request.  K's slices are a
   // contiguous prefix of its block, so a range of ns * 256 bytes reads the
@@ -166,40 +159,51 @@ void decode_kernel(DecodeArgs a) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int g = lane & 15;
+  const int p_begin = s * a.pages_per_split;
+  // wave w takes the groups of kDecUnroll pages that start at p_begin + kDecUnroll * (w + kDecWaves * i).
+  constexpr int kStride = kDecUnroll * kDecWaves;
+  const int p_first = p_begin + kDecUnroll * __builtin_amdgcn_readfirstlane(wave);
+  // The first group's page-table entries are fetched together with the
+  // sequence length, their index clamped into the table row only (an entry
+  // past the split is never used), so the first page loads wait for two
+  // memory round trips after the kernel arguments, not three.
+  int ent[kDecUnroll];
+  {
+    const int* row = a.page_table + static_cast<int64_t>(b) * a.max_pages;
+#pragma unroll
+    for (int u = 0; u < kDecUnroll; ++u) ent[u] = row[min(p_first + u, a.max_pages - 1)];
+  }
   const int N = max(0, min(a.seq_lens[b], a.max_seq_len));
   const int n_pages = (N + kPage - 1) / kPage;
-  const int p_begin = s * a.pages_per_split;
   const int p_end = min(n_pages, p_begin + a.pages_per_split);
   const float NEG_INF = -__builtin_huge_valf();
   const float c = a.scale_log2;
 
-  // wave w takes the groups of kDecUnroll pages that start at p_begin + kDecUnroll * (w + kDecWaves * i).
   // The first group's page loads are issued before Q is loaded and rotated, so
-  // the wave's first memory round trip overlaps the Q work; each later group
-  // is loaded into the same registers right after the previous one is used.
-  constexpr int kStride = kDecUnroll * kDecWaves;
-  int ent[kDecUnroll];
+  // the wave's first memory round trip overlaps the Q work.  Each page's
+  // registers are loaded with the page one stride on right after the page is
+  // used, so a wave keeps kDecUnroll - 1 to kDecUnroll pages in flight.
   PageRegs pr[kDecUnroll];
-  const int p_first = p_begin + kDecUnroll * __builtin_amdgcn_readfirstlane(wave);
   // per-key rule: slice walkers for the youngest (offset 15) and oldest key of a page
   SliceWalker wy, wo;
   if constexpr (kPerKey) {
     wy.init(a.st, (N - 1) - (kPage - 1));
     wo.init(a.st, N - 1);
   }
-  if (p_first < p_end) {
-    dec_fetch_group(a, b, p_first, p_begin, p_end, ent);
+  // Straight-line code up to the first page loads of the level rule (a page
+  // past the split gets an empty buffer range: its loads return zeros without
+  // a memory request), so the compiler reads every kernel argument they need in
+  // the first batch.  (The per-key rule's walkers branch; counting its first
+  // group's slices branch-free instead cost more than it saved.)
 #pragma unroll
-    for (int u = 0; u < kDecUnroll; ++u) {
-      if (p_first + u < p_end) {
-        int ns;
-        bool mask;
-        page_slices<kPerKey>(a, wy, wo, p_first + u, N, ns, mask);
-        dec_load_page(a, h, ent[u], p_first + u, ns, mask, lane, pr[u]);
-      }
-    }
-    dec_fetch_group(a, b, p_first + kStride, p_begin, p_end, ent);
+  for (int u = 0; u < kDecUnroll; ++u) {
+    int ns;
+    bool mask;
+    page_slices<kPerKey>(a, wy, wo, p_first + u, N, ns, mask);
+    dec_load_page(a, h, ent[u], p_first + u < p_end, p_first + u, ns, mask, lane, pr[u]);
   }
+#pragma unroll
+  for (int u = 0; u < kDecUnroll; ++u) ent[u] = dec_fetch_entry(a, b, p_first + kStride + u, p_begin, p_end);
 
   // ---- Q^T fragments: lane holds q head g, slice 4 lp + lane/16 ----
   u32x4 Qf[4];
@@ -303,19 +307,15 @@ void decode_kernel(DecodeArgs a) {
         O[db] *= alpha;
         O[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, r.v[db]), pb, O[db], 0, 0, 0);
       }
-    }
-    const int pn = p0 + kStride;
-    if (pn < p_end) {
-#pragma unroll
-      for (int u = 0; u < kDecUnroll; ++u) {
-        if (pn + u < p_end) {
-          int ns;
-          bool mask;
-          page_slices<kPerKey>(a, wy, wo, pn + u, N, ns, mask);
-          dec_load_page(a, h, ent[u], pn + u, ns, mask, lane, pr[u]);
-        }
+      // this page's registers take the page one stride on
+      const int pn = p0 + kStride + u;
+      if (pn < p_end) {
+        int ns;
+        bool mask;
+        page_slices<kPerKey>(a, wy, wo, pn, N, ns, mask);
+        dec_load_page(a, h, ent[u], true, pn, ns, mask, lane, pr[u]);
+        ent[u] = dec_fetch_entry(a, b, pn + kStride, p_begin, p_end);
       }
-      dec_fetch_group(a, b, pn + kStride, p_begin, p_end, ent);
     }
   }
 
@@ -380,7 +380,20 @@ void decode_kernel(DecodeArgs a) {
 constexpr int kMergeChunks = 4;
 constexpr int kMergeDims = kD / kMergeChunks;  // 32
 
-__global__ __launch_bounds__(kDecWaves * 64) void decode_merge_kernel(DecodeArgs a) {
+// The merge kernel's arguments: a block of its own, every field used before
+// the first branch, so the kernel reads them in one memory round trip (with
+// the decode kernel's argument block, the fields read behind branches cost a
+// second dependent round trip before the partials could be requested).
+struct MergeArgs {
+  const float* ws_ml;
+  const float* ws_o;
+  uint16_t* out;
+  int64_t o_sb, o_sh;
+  int n_splits, group, hkv;
+  float scale_log2;
+};
+
+__global__ __launch_bounds__(512) void decode_merge_kernel(MergeArgs a) {
   __shared__ __attribute__((aligned(16))) float sh_o[64 * kMergeDims];
   __shared__ float red[2 * 64];
   const int chunk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -473,7 +486,8 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t s) {
     hipLaunchKernelGGL(decode_kernel<false>, dim3(a.n_splits, a.hkv, a.batch), dim3(kDecWaves * 64), 0, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.n_splits == 1) return e;
-  hipLaunchKernelGGL(decode_merge_kernel, dim3(kMergeChunks, a.hkv, a.batch), dim3(kDecWaves * 64), 0, s, a);
+  const MergeArgs m{a.ws_ml, a.ws_o, a.out, a.o_sb, a.o_sh, a.n_splits, a.group, a.hkv, a.scale_log2};
+  hipLaunchKernelGGL(decode_merge_kernel, dim3(kMergeChunks, a.hkv, a.batch), dim3(512), 0, s, m);
   return hipGetLastError();
 }
 
