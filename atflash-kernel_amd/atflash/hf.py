@@ -114,9 +114,17 @@ class PagedLayer(CacheLayerMixin):
         self.length = self.prev_length = 0
         self.last_key = None
 
-    def crop(self, tokens_to_remove: int) -> None:
-        n = abs(int(tokens_to_remove)) if tokens_to_remove <= 0 else self.length - int(tokens_to_remove)
-        self.length = max(0, self.length - max(0, n))
+    def crop(self, max_length: int) -> None:
+        """Keep the first max_length tokens (max_length < 0: drop the last
+        |max_length|), as HF's DynamicLayer.crop.  The pages keep their
+        contents; positions past the new length are rewritten by the next
+        update before anything reads them."""
+        max_length = int(max_length)
+        if max_length < 0:
+            max_length = self.length - abs(max_length)
+        if self.length <= max_length:
+            return
+        self.length = max(0, max_length)
         self.prev_length = min(self.prev_length, self.length)
         self.last_key = None
 
