@@ -128,9 +128,13 @@ __device__ __forceinline__ void dec_load_page(const DecodeArgs& a, int h, int ra
   // base, 32-bit lane offset, immediate row offset, no per-load address
   // arithmetic.  Every page is read once per call, so the loads are
   // non-temporal.
+  // (The range goes through readfirstlane: the level count is uniform, but the
+  // compiler may count it in a vector register, and a resource built from one
+  // becomes a loop over lanes around every load.)
   const size_t blk_bytes = (static_cast<size_t>(ok ? pg : 0) * a.hkv + h) * (kBlockElems * 2);
+  const int k_range = __builtin_amdgcn_readfirstlane(ok ? ns * (kPage * kSliceDims * 2) : 0);
   const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(a.k_cache) + blk_bytes / 2, 0, ok ? ns * (kPage * kSliceDims * 2) : 0, kBufferWord3);
+      const_cast<uint16_t*>(a.k_cache) + blk_bytes / 2, 0, k_range, kBufferWord3);
   const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(a.v_cache) + blk_bytes / 2, 0, ok ? kBlockElems * 2 : 0, kBufferWord3);
   // K: slice 4 lp + lane/16, token lane%16: quad lp is the 1 KB run at lp * 1024
