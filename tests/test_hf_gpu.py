@@ -174,3 +174,27 @@ def test_model_chunked_prefill_equals_single_shot(mode, dev):
           f"layer-0 K bitwise {torch.equal(k1, k2)} max|d| {kd:.3e}", flush=True)
     assert torch.equal(single, chunked) and torch.equal(k1, k2)
     hf.unregister(model)
+
+
+def test_generate_with_paged_cache_equals_dynamic_cache(dev):
+    """transformers' generate() with the hook's PagedCache as past_key_values
+    (prefill and decode on the persistent pages) gives the same greedy tokens
+    and the same logits, bit for bit, as generate() with HF's DynamicCache,
+    where the hook packs the history into a temporary paged cache per call:
+    both run the same kernels on identical pages."""
+    model = _model(dev)
+    hook = hf.register(model, K_RET, K_RET, n_ctx=4096, mode="win")
+    ids = torch.randint(0, 512, (1, N), generator=torch.Generator().manual_seed(5)).to(dev)
+    kw = dict(max_new_tokens=6, do_sample=False, pad_token_id=0, return_dict_in_generate=True, output_logits=True,
+              attention_mask=torch.ones_like(ids))
+    with torch.no_grad():
+        dyn = model.generate(ids, **kw)
+        cache = hook.new_cache(model.config, 1, N + 8, dev)
+        paged = model.generate(ids, past_key_values=cache, **kw)
+    print(f"[hf generate] tokens dynamic {dyn.sequences[0, N:].tolist()} paged {paged.sequences[0, N:].tolist()}",
+          flush=True)
+    assert torch.equal(dyn.sequences, paged.sequences)
+    for a, b in zip(dyn.logits, paged.logits):
+        assert torch.equal(a, b)
+    assert cache.get_seq_length() == N + 5  # the last generated token is not fed back
+    hf.unregister(model)
