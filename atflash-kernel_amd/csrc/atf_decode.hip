@@ -185,8 +185,12 @@ void decode_kernel(DecodeArgs a) {
 
   // The first group's page loads are issued before Q is loaded and rotated, so
   // the wave's first memory round trip overlaps the Q work.  Each page's
-  // registers are loaded with the page one stride on right after the page is
-  // used, so a wave keeps kDecUnroll - 1 to kDecUnroll pages in flight.
+  // registers are reloaded with the page one stride on right after the page is
+  // used, so the next group's loads go out while the rest of the group is
+  // computed.  (A group still starts with a wait for all of its loads: the
+  // reloads are conditional on the split's end.  Issuing every load on every
+  // path, so that each page is waited for with the later pages' loads still in
+  // flight, measured slower.)
   PageRegs pr[kDecUnroll];
   // per-key rule: slice walkers for the youngest (offset 15) and oldest key of a page
   SliceWalker wy, wo;
