@@ -633,8 +633,12 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
     const int rows_a = copies_v ? 4 : (w_ld.advance(a.lt, ct) + 1) >> 1;
     const int rows_b = copies_v ? 4 : (w_ld.advance(a.lt, ct + 1) + 1) >> 1;
     const int pa = page_id(a, pg_a), pb = page_id(a, pg_b);
+    // The wave's two pages are copied in two batches, the first here and the
+    // second halfway through the softmax: the four waves of the group issue
+    // their copies together, and a wave issuing all eight 1 KB rows at once
+    // waits for the CU's texture path to take them (k=2 -0.4 to -0.9%, OFF
+    // unchanged against issuing both pages here).
     if (ct < lim) stage_page(cbase, pstride, pa, rows_a, cdst, lane, copy_off);
-    if (ct + 1 < lim) stage_page(cbase, pstride, pb, rows_b, cdst + kPfSlotBytes, lane, copy_off);
     if (2 * u < t_end) {
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
@@ -663,7 +667,14 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
       // max taken: where it exceeds m_ref by more than 8 (always on the first
       // pair), m_ref moves up to it, O and l are rescaled, and the pair's P is
       // computed again from the shifted scores (shift 0 for the other lanes).
-      float lt = exp_tiles<kRaw>(S, Pf, c);
+      float lt = 0.f;
+      exp_block<kRaw>(S[0], Pf[0], Pf[1], c, lt);
+      exp_block<kRaw>(S[1], Pf[2], Pf[3], c, lt);
+      __builtin_amdgcn_sched_barrier(0);
+      if (ct + 1 < lim) stage_page(cbase, pstride, pb, rows_b, cdst + kPfSlotBytes, lane, copy_off);
+      __builtin_amdgcn_sched_barrier(0);
+      exp_block<kRaw>(S[2], Pf[4], Pf[5], c, lt);
+      exp_block<kRaw>(S[3], Pf[6], Pf[7], c, lt);
       if (__builtin_amdgcn_ballot_w64((u == 0) || !(lt <= 256.f)) != 0) {
         float mx = NEG_INF;
 #pragma unroll
@@ -694,6 +705,7 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
       }
       l_run += lt;
     } else {
+      if (ct + 1 < lim) stage_page(cbase, pstride, pb, rows_b, cdst + kPfSlotBytes, lane, copy_off);
 #pragma unroll
       for (int i = 0; i < 8; ++i) Pf[i] = bf16x8{};
     }
