@@ -20,6 +20,11 @@ Pins (each checked in tests/test_oracle_tables.py):
                       that differs from the reference's binary search, and a
                       brute-force scan over every z < cap pins it on small caps.
   zhi_slice_vec8      c1_window_tables.txt FI rows and mma_slices.fi_zhi8.
+  zhi_pair            every 4th entry is the vec8 entry of its slice (the
+                      pinned table), and its pairs' entries are non-increasing
+                      within a slice; the width-2 decode it drives is pinned by
+                      an fp64 per-key, per-pair brute force
+                      (tests/test_oracle_attention.py).
   theory_s_vec8       mma_slices.fi_s_bar at at_len.
   mma_slice_stats     microbench/7b_prefill_mb.json qk_slice_ratio_s and
                       b1_bench_A*.json qk_slice_ratio_theory / kload_dim_ratio_theory.
@@ -130,6 +135,13 @@ def levels_of_zmin(z: int, zhi) -> int:
     """Number of 16-dim levels read at distance z: D_eff(z) / 16 through the
     identity D_eff(z) = 16 * #{i : zhi[i] >= z} (microbench/b1_correctness.py:43-44)."""
     return max(1, sum(1 for t in zhi if t >= z))
+
+
+def zhi_pair(head_dim, rope_base, k_ret) -> list:
+    """Per-pair decode table of the reference's gate: floor(w'_j) for every
+    sorted pair j, INT32_MAX for an infinite width (gates/g2_correctness.py:73-76)."""
+    w = wavelengths_sorted(head_dim, rope_base, k_ret)
+    return [INT32_MAX if math.isinf(x) else min(INT32_MAX, int(math.floor(x))) for x in w]
 
 
 def zhi_slice_vec8(head_dim, rope_base, k_ret) -> list:

@@ -225,6 +225,29 @@ def test_sliced_decode_vec8_with_paired_entries_equals_width_16():
     assert all(z8[2 * lv] == zhi16[lv] and z8[2 * lv + 1] <= z8[2 * lv] for lv in trimmed)
 
 
+def test_sliced_decode_per_pair_equals_fp64_brute_force():
+    """2-dim slices (the per-pair table of the reference's gate,
+    gates/g2_correctness.py:73-76) against the key-by-key fp64 brute force,
+    with a planted off-by-one that must differ.  The per-pair table holds the
+    vec8 table's entry on the first pair of each 8-dim slice and smaller ones
+    on the other three, so it reads a subset of what vec8 reads."""
+    N = 260
+    zp = WR.zhi_pair(D, 1e4, 0.3)
+    z8 = WR.zhi_slice_vec8(D, 1e4, 0.3)
+    assert [zp[4 * t] for t in range(16)] == list(z8)
+    assert all(zp[4 * t + i] <= z8[t] for t in range(16) for i in range(4))
+    assert len(set(z for z in zp if z < N)) > 10  # many boundaries inside the context
+    q, k, v = _rand((4, D), 46), _rand((N, 2, D), 47), _rand((N, 2, D), 48)
+    got, _ = OA.ref_decode_sliced(q, k, v, zp, 2)
+    ref = _sliced_decode_fp64(q, k, v, zp, 2)
+    assert (got.double() - ref).abs().max().item() < 1e-5
+    planted = _sliced_decode_fp64(q, k, v, zp, 2, shift=1)
+    assert (got.double() - planted).abs().max().item() > 1e-3
+    # the finer table drops terms vec8 keeps, so the results differ
+    g8, _ = OA.ref_decode_sliced(q, k, v, z8, 8)
+    assert (got - g8).abs().max().item() > 1e-3
+
+
 def test_lse_merge_equals_unsplit():
     s = _rand((3, 200), 31) * 3
     vv = _rand((200, D), 32)
