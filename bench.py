@@ -204,11 +204,12 @@ def bench_detail(steps=3):
     """The other published configurations, each window OFF and k = 2 with the
     ON/OFF ratio beside the reference's: Llama-3.2-3B prefill (24/8 heads, base
     5e5) at 8K/32K/128K; Llama decode at batch 1 and 8 over 8K-160K (paged,
-    permuted pages, pools of >= 1 GiB rotated); Qwen2.5-7B prefill of 512K
-    tokens in 8K query chunks against the growing cache (attention only, the
-    cache pre-filled)."""
+    permuted pages, pools of >= 1 GiB rotated); Qwen2.5-7B prefill of 32K, 262K
+    and 512K tokens in 8K query chunks against the growing cache (attention
+    only, the cache pre-filled); Qwen2.5-7B decode at 512K (level and vec8
+    tables)."""
     import torch
-    from atflash import atflash_window as AW, interface, ops, rope as R
+    from atflash import atflash_window as AW, fiwin_common as FW, interface, ops, rope as R
     from atflash.cache import PagedKVCache
     dev = torch.device("cuda:0")
     out = {"llama_prefill": {}, "llama_decode": {}, "qwen_prefill_chunked": {}}
@@ -280,29 +281,61 @@ def bench_detail(steps=3):
             del pool, tables, q, rt
             torch.cuda.empty_cache()
 
-    # ---- Qwen2.5-7B prefill of 512K tokens in 8K query chunks ----
-    N, C = 524288, 8192
-    g = torch.Generator(device=dev).manual_seed(512)
-    q = torch.randn((1, N, HQ, D), generator=g, device=dev).to(torch.bfloat16)
-    k = torch.randn((1, N, HKV, D), generator=g, device=dev).to(torch.bfloat16)
-    v = torch.randn((1, N, HKV, D), generator=g, device=dev).to(torch.bfloat16)
+    # ---- Qwen2.5-7B prefill of 32K, 262K and 512K tokens in 8K query chunks ----
+    C = 8192
+    for N in (32768, 262144, 524288):
+        g = torch.Generator(device=dev).manual_seed(N // 1024)
+        q = torch.randn((1, N, HQ, D), generator=g, device=dev).to(torch.bfloat16)
+        k = torch.randn((1, N, HKV, D), generator=g, device=dev).to(torch.bfloat16)
+        v = torch.randn((1, N, HKV, D), generator=g, device=dev).to(torch.bfloat16)
+        rt = R.rope_table(N, R.inv_freq(D, BASE, dev))
+        kc, vc, table = interface.pack_kv(k, v, rope=rt)
+        del k, v
+        r = {}
+        for name, zhi in (("off", None), ("k2", list(AW.window_zhi_from_kret(D, BASE, 2.0, 1 << 23)))):
+            def fn():
+                for c0 in range(0, N, C):
+                    ops.prefill(q[:, c0:c0 + C], kc, vc, table, c0 + C, c0, zhi, D ** -0.5, rt, 0)
+            fn()
+            r[name + "_ms"] = statistics.median(_events_time(fn, 2))
+        r["on_over_off"] = r["off_ms"] / r["k2_ms"]
+        r.update(_ref_ratio("qwen_prefill_ms", N))
+        r["reference_note"] = "reference: single-shot FA4 (its stock OFF degrades past 256K)"
+        out["qwen_prefill_chunked"][N] = r
+        print(f"[bench detail] qwen prefill {N // 1024}K in 8K chunks: off {r['off_ms']:.1f} ms k2 {r['k2_ms']:.1f} ms "
+              f"({r['on_over_off']:.3f}x; reference {r['reference_ratio']:.3f}x)", flush=True)
+        del q, kc, vc, table, rt
+        torch.cuda.empty_cache()
+
+    # ---- Qwen2.5-7B decode at 512K (batch 1, permuted pages, one 2 GB pool) ----
+    N = 524288
+    pages = N // 16
     rt = R.rope_table(N, R.inv_freq(D, BASE, dev))
-    kc, vc, table = interface.pack_kv(k, v, rope=rt)
-    del k, v
-    r = {}
-    for name, zhi in (("off", None), ("k2", list(AW.window_zhi_from_kret(D, BASE, 2.0, 1 << 23)))):
-        def fn():
-            for c0 in range(0, N, C):
-                ops.prefill(q[:, c0:c0 + C], kc, vc, table, c0 + C, c0, zhi, D ** -0.5, rt, 0)
-        fn()
-        r[name + "_ms"] = statistics.median(_events_time(fn, 2))
-    r["on_over_off"] = r["off_ms"] / r["k2_ms"]
-    r.update(_ref_ratio("qwen_prefill_ms", N))
-    r["reference_note"] = "reference: single-shot FA4 (stock OFF degrades past 256K)"
-    out["qwen_prefill_chunked"][N] = r
-    print(f"[bench detail] qwen prefill 512K in 8K chunks: off {r['off_ms']:.0f} ms k2 {r['k2_ms']:.0f} ms "
-          f"({r['on_over_off']:.3f}x; reference {r['reference_ratio']:.3f}x)", flush=True)
-    del q, kc, vc, table, rt
+    pool = PagedKVCache(pages, HKV, dev)
+    tab = torch.randperm(pages, generator=torch.Generator().manual_seed(5)).to(torch.int32).view(1, -1).to(dev)
+    g = torch.Generator(device=dev).manual_seed(5)
+    for c0 in range(0, N, 131072):  # written in 128K pieces to bound the temporaries
+        k = torch.randn((1, 131072, HKV, D), generator=g, device=dev).to(torch.bfloat16)
+        v = torch.randn((1, 131072, HKV, D), generator=g, device=dev).to(torch.bfloat16)
+        torch.ops.atflash.kv_write(pool.k, pool.v, k, v, torch.full((1,), c0, dtype=torch.int32, device=dev), tab,
+                                   rt, 0)
+        del k, v
+    q = torch.randn((1, HQ, D), generator=g, device=dev).to(torch.bfloat16)
+    seq = torch.tensor([N], dtype=torch.int32, device=dev)
+    r = {"kv_pool_bytes": pages * HKV * 8192}
+    for name, zhi in (("off", None), ("k2", list(AW.window_zhi_from_kret(D, BASE, 2.0, 1 << 23))),
+                      ("k2_vec8", FW.zhi_slice_vec8(D, BASE, 2.0).tolist())):
+        fn = lambda: ops.decode_paged(q, pool.k, pool.v, tab, seq, N, zhi, D ** -0.5, rt, 0)  # noqa: E731
+        for _ in range(10):
+            fn()
+        r[name + "_us"] = _events_time_batch(fn, 20 * steps) * 1e3
+    r["on_over_off"] = r["off_us"] / r["k2_us"]
+    r["on_over_off_vec8"] = r["off_us"] / r["k2_vec8_us"]
+    r["off_frac_of_8TBs"] = N * HKV * D * 2 * 2 / (r["off_us"] * 1e-6) / PEAK_HBM
+    out["qwen_decode"] = {N: r}
+    print(f"[bench detail] qwen decode 512K: off {r['off_us']:.1f} us k2 {r['k2_us']:.1f} us ({r['on_over_off']:.3f}x), "
+          f"k2 vec8 {r['k2_vec8_us']:.1f} us; OFF {r['off_frac_of_8TBs']:.3f} of 8 TB/s", flush=True)
+    del pool, tab, q, rt
     torch.cuda.empty_cache()
     return out
 
