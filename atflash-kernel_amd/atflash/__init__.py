@@ -5,7 +5,7 @@
     atflash_window  torch-free twin that emits the kernels' level table `zhi`
     fiwin_common    decode-side tables (vec8 slices, s-bar)
     rope            RoPE tables for RoPE-at-load
-    cache           paged KV cache in the kernels' level-blocked layout
+    cache           paged KV cache in the kernels' slice-blocked layout
     ops             torch.library operators over the HIP C ABI
     interface       reference-shaped entry points (_flash_attn_fwd, decode)
     model_tables    window and RoPE tables from a model config (rope scaling
