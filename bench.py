@@ -12,7 +12,7 @@ bf16 N(0,1) synthetic tensors from a fixed seed.
            N tokens whose pages are randomly permuted; four cache copies (> 1 GiB)
            are rotated so the 256 MB MALL cannot hold the working set;
   kv_write the paged-cache writer over the same N tokens (K rotated and
-           level-blocked, V transposed into pages), timed as one batch of 4*K
+           slice-blocked, V transposed into pages), timed as one batch of 4*K
            back-to-back launches (`roofline_kv_write`, HBM bound).
 A step is one such call.  W untimed warm-up steps, then exactly K timed steps per
 configuration (decode: 40*K), each bracketed by HIP events on the launch
