@@ -380,11 +380,12 @@ void decode_kernel(DecodeArgs a) {
 // workgroup per (sequence, kv head) issued 4x as many loads from one CU and
 // took about as long as the tail it replaced.  Thread t takes dims
 // 32 * chunk + 4 * (t % 8) .. +3 of query head mg and every H-th split
-// starting at hh (H as large as G * H <= 64 allows, so the split loop is
-// short).  It loads the (m, l) and o of up to kBatch splits before using any
-// of them, so with up to 32 splits per thread the merge costs one memory round
-// trip; more splits are folded in batch by batch with a running max.  The H
-// partial merges of a (head, dims) are combined through LDS.
+// starting at hh (H = 8 split groups for G <= 8, 4 for larger groups).  It
+// loads the (m, l) and o of up to kBatch splits before using any of them, so
+// with up to 32 splits per thread the merge costs one memory round trip; more
+// splits are folded in batch by batch with a running max.  The H partial
+// merges of a (head, dims) sit in lanes of one wave and are combined by
+// cross-lane exchanges, without LDS or a workgroup barrier.
 constexpr int kMergeChunks = 4;
 constexpr int kMergeDims = kD / kMergeChunks;  // 32
 
@@ -401,16 +402,34 @@ struct MergeArgs {
   float scale_log2;
 };
 
+// One (m, l, o) partial merged with the partial of lane ^ mask (a cross-lane
+// exchange within the wave, no LDS): both lanes end up holding the merge.
+__device__ __forceinline__ void merge_xor(float& m, float& l, f32x4& o, int mask, float c) {
+  const float NEG_INF = -__builtin_huge_valf();
+  const float mp = __shfl_xor(m, mask), lp = __shfl_xor(l, mask);
+  f32x4 op;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) op[i] = __shfl_xor(o[i], mask);
+  const float M = fmaxf(m, mp);
+  if (M != NEG_INF) {
+    const float w = fast_exp2((m - M) * c), wp = fast_exp2((mp - M) * c);  // an empty side: m = -inf -> 0
+    l = w * l + wp * lp;
+    o = w * o + wp * op;
+    m = M;
+  }
+}
+
 __global__ __launch_bounds__(512) void decode_merge_kernel(MergeArgs a) {
-  __shared__ __attribute__((aligned(16))) float sh_o[64 * kMergeDims];
-  __shared__ float red[2 * 64];
   const int chunk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x;
   const float NEG_INF = -__builtin_huge_valf();
   const float c = a.scale_log2;
   const int64_t pbase = (static_cast<int64_t>(b) * a.hkv + h) * a.n_splits * kDecMaxGroup;  // split 0, head 0
   constexpr int kBatch = 32;
-  const int H = (a.group <= 1) ? 64 : (a.group <= 2) ? 32 : (a.group <= 4) ? 16 : (a.group <= 8) ? 8 : 4;
+  // H split groups per (head, dims), 8 threads per group (4 dims each): the H
+  // groups of a head are lanes 8 hh + (t % 8) of one wave (H = 8 for G <= 8,
+  // 4 for larger groups), so their partial merges combine across lanes.
+  const int H = (a.group <= 8) ? 8 : 4;
   const int row = tid >> 3;  // 0..63: (head, split group)
   const int mg = row / H, hh = row - (row / H) * H;
   const int q4 = 4 * (tid & 7);
@@ -449,30 +468,18 @@ __global__ __launch_bounds__(512) void decode_merge_kernel(MergeArgs a) {
         m_t = mb;
       }
     }
-    *reinterpret_cast<f32x4*>(&sh_o[row * kMergeDims + q4]) = acc_t;
-    if (q4 == 0) {
-      red[row] = m_t;
-      red[64 + row] = L_t;
-    }
   }
-  __syncthreads();
+  // every lane of the wave takes part in the exchanges (inactive rows hold an
+  // empty partial)
+  merge_xor(m_t, L_t, acc_t, 8, c);
+  merge_xor(m_t, L_t, acc_t, 16, c);
+  if (H == 8) merge_xor(m_t, L_t, acc_t, 32, c);
   if (mact && hh == 0) {
-    float M = NEG_INF;
-    for (int h2 = 0; h2 < H; ++h2) M = fmaxf(M, red[row + h2]);
-    float L = 0.f;
-    f32x4 o = f32x4{};
-    if (M != NEG_INF) {
-      for (int h2 = 0; h2 < H; ++h2) {
-        const float wt = fast_exp2((red[row + h2] - M) * c);
-        L += wt * red[64 + row + h2];
-        o += wt * *reinterpret_cast<const f32x4*>(&sh_o[(row + h2) * kMergeDims + q4]);
-      }
-    }
-    const float inv = L > 0.f ? 1.f / L : 0.f;
+    const float inv = L_t > 0.f ? 1.f / L_t : 0.f;
     uint16_t* out = a.out + static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(h * a.group + mg) * a.o_sh + md4;
     u32x2 pk;
-    pk[0] = pack_bf16x2(o[0] * inv, o[1] * inv);
-    pk[1] = pack_bf16x2(o[2] * inv, o[3] * inv);
+    pk[0] = pack_bf16x2(acc_t[0] * inv, acc_t[1] * inv);
+    pk[1] = pack_bf16x2(acc_t[2] * inv, acc_t[3] * inv);
     *reinterpret_cast<u32x2*>(out) = pk;
   }
 }
