@@ -6,7 +6,10 @@ chunk of any length at the bottom-right end (offsets not multiples of the
 32-row tile included), RoPE at load or pre-rotated input, window OFF or k in
 {0.05, 0.5, 2, 64} at three RoPE bases.  Decode: batch 1-3 with ragged lengths
 up to 3000 on randomly permuted pages of one pool, the level table (page rule)
-or the vec8 table (per-key rule), window OFF included.  The draws are printed
+or the vec8 table (per-key rule), window OFF included; a second decode draw
+takes contexts of 3000-60000 tokens and groups up to 16 (9 and 12 included),
+so that the split merge runs with many splits in both of its lane layouts
+(eight split groups per head for G <= 8, four above).  The draws are printed
 before each case runs."""
 import random
 
@@ -31,7 +34,7 @@ def _prefill_case(seed):
     return B, hkv, G, nk, nq, r.choice(BASES), r.choice(KS), r.random() < 0.75
 
 
-@pytest.mark.parametrize("seed", range(12))
+@pytest.mark.parametrize("seed", range(32))
 def test_random_prefill_matches_oracle(seed, dev):
     from atflash import atflash_window as AW, interface, rope as R
     B, hkv, G, nk, nq, base, k_ret, rope = _prefill_case(seed)
@@ -58,13 +61,30 @@ def _decode_case(seed):
     return B, hkv, G, lens, r.choice(BASES), r.choice(KS), r.choice(("level", "vec8"))
 
 
-@pytest.mark.parametrize("seed", range(12))
+def _long_decode_case(seed):
+    r = random.Random(77_000 + seed)
+    B = r.randint(1, 2)
+    hkv = r.choice((1, 2, 4))
+    G = r.choice((3, 7, 8, 9, 12, 16))
+    lens = [r.randint(3000, 60000) for _ in range(B)]
+    return B, hkv, G, lens, r.choice(BASES), r.choice(KS), r.choice(("level", "vec8"))
+
+
+@pytest.mark.parametrize("seed", range(32))
 def test_random_decode_matches_oracle(seed, dev):
+    _run_decode(f"random decode {seed}", seed, _decode_case(seed), dev)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_long_decode_matches_oracle(seed, dev):
+    _run_decode(f"random long decode {seed}", seed, _long_decode_case(seed), dev)
+
+
+def _run_decode(name, seed, case, dev):
     from atflash import atflash_window as AW, fiwin_common as FW, interface, rope as R
     from atflash.cache import PagedKVCache
-    B, hkv, G, lens, base, k_ret, table_kind = _decode_case(seed)
-    print(f"[random decode {seed}] B={B} hkv={hkv} G={G} lens={lens} base={base:g} k={k_ret} table={table_kind}",
-          flush=True)
+    B, hkv, G, lens, base, k_ret, table_kind = case
+    print(f"[{name}] B={B} hkv={hkv} G={G} lens={lens} base={base:g} k={k_ret} table={table_kind}", flush=True)
     hq = G * hkv
     total_pages = sum(-(-n // 16) for n in lens) + 5
     cache = PagedKVCache(total_pages, hkv, dev)
@@ -94,5 +114,5 @@ def test_random_decode_matches_oracle(seed, dev):
             ref = H.decode_oracle_vec8(q[b], k[0], v[0], base, zhi, True)
         else:
             ref = H.decode_oracle(q[b], k[0], v[0], base, float("inf") if k_ret is None else k_ret, True)
-        mx, mean = H.assert_close(out[b], ref, f"random decode {seed} seq {b} len {lens[b]}")
+        mx, mean = H.assert_close(out[b], ref, f"{name} seq {b} len {lens[b]}")
     print(f"  last seq max {mx:.3e} mean {mean:.3e}", flush=True)
