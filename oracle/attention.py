@@ -17,7 +17,10 @@ Pins (tests/test_oracle_attention.py):
   * q_offset chunks equal the single-shot rows;
   * GQA equals an explicit repeat of K/V heads;
   * rope_hf equals complex multiplication by e^{i pos theta} (the textbook
-    definition), and the sorted-pair permutation makes the window a prefix.
+    definition), and the sorted-pair permutation makes the window a prefix;
+  * mode="bf16" rounds P to bf16 (round to nearest even) before P @ V: a
+    two-key case with a closed-form softmax gives bf16(P0) - bf16(P1) exactly,
+    and rounding only the output would not.
 ref_decode_sliced follows gates/g2_correctness.py:43-70 and is pinned against
 ref_window_attn(phase="decode") where the two granularities coincide (slice
 tables built from a tile-quantized rule at block_n = 1).

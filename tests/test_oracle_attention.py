@@ -118,6 +118,44 @@ def test_bf16_mode_is_an_anchor_near_fp32():
     assert (a - b.float()).abs().max().item() < 2e-2
 
 
+def _bf16_rne(x: float) -> float:
+    """Round a float to bfloat16 by round-to-nearest-even on its fp32 bits."""
+    import numpy as np
+    a = int(np.array(x, dtype=np.float32).view(np.uint32))
+    a = ((a + 0x7FFF + ((a >> 16) & 1)) >> 16) << 16
+    return float(np.array(a, dtype=np.uint32).view(np.float32))
+
+
+def test_bf16_mode_rounds_p_to_bf16_before_pv_closed_form():
+    """bf16 mode (atflash/reference.py:27-80, P.to(bf16) @ V) on a case with a
+    closed form: one query, two keys with exact bf16 scores 0 and 1 (a single
+    non-zero product each), so P = (1, e^s) / (1 + e^s) with s = 1/sqrt(128).
+    With V columns (1, -1) and (1, 0) the outputs are bf16(P0) - bf16(P1) and
+    bf16(P0), the probabilities rounded to bf16 (round to nearest even) before
+    the product.  Both P sit more than 7e-4 (relative) from a bf16 rounding
+    boundary, far above fp32 error.  A mode that rounded only the output (the
+    fp32 result cast to bf16) gives -0.04419 for the first column instead of
+    -0.044921875, which the last assertion shows."""
+    q = torch.zeros((1, 1, 1, D), dtype=torch.bfloat16)
+    k = torch.zeros((1, 1, 2, D), dtype=torch.bfloat16)
+    v = torch.zeros((1, 1, 2, D), dtype=torch.bfloat16)
+    q[0, 0, 0, 0] = 1.0
+    k[0, 0, 1, 0] = 1.0
+    v[0, 0, 0, 0], v[0, 0, 1, 0] = 1.0, -1.0
+    v[0, 0, 0, 1] = 1.0
+    w = WR.wavelengths_sorted(D, 1e4, 2.0)
+    got = OA.ref_window_attn(q, k, v, w, phase="decode", block_m=1, block_n=1, mode="bf16")[0, 0, 0]
+    s = 1.0 / math.sqrt(D)
+    p0, p1 = 1.0 / (1.0 + math.exp(s)), math.exp(s) / (1.0 + math.exp(s))
+    r0, r1 = _bf16_rne(p0), _bf16_rne(p1)
+    assert (r0, r1) == (0.478515625, 0.5234375)
+    assert got[0].item() == r0 - r1 == -0.044921875
+    assert got[1].item() == r0
+    assert got[2:].abs().max().item() == 0.0
+    late = OA.ref_window_attn(q, k, v, w, phase="decode", block_m=1, block_n=1, mode="fp32")[0, 0, 0]
+    assert late[0].to(torch.bfloat16).item() != got[0].item()
+
+
 def test_rope_hf_equals_complex_rotation():
     x = _rand((3, 10, D), 25)
     pos = torch.arange(100, 110)
