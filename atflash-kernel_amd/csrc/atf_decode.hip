@@ -13,7 +13,8 @@
 // The window table is per 8-dim slice (16 entries; a 16-dim level table is
 // passed as each level's value for its two slices).  Page p is read for the
 // first n(p) = #{s : zhi8[s] >= (N-1) - (16p+15)} slices, those its youngest
-// key reads; the loads of the other slices are never issued, so out-of-window
+// key reads: the page's K buffer range covers those slices only, so the loads
+// of the other slices return zeros without a memory request and out-of-window
 // K bytes are not read from HBM.  Page rule (level table, block_n = 16): every
 // key of the page uses those slices.  Per-key rule (vec8 table, as the
 // FlashInfer port's decode, kernels/flashinfer_port/decode.cuh.diff:47-89):
