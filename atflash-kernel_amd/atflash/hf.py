@@ -30,13 +30,19 @@ view of the DynamicCache tensors, e2e:100-110).  The kernels here read a paged,
 slice-blocked cache instead, so the serving path is `PagedCache`: an HF `Cache`
 whose per-layer `update` appends the new keys and values to that layer's pages
 with the cache-writer kernel (rotating K there with rope_at_load) and returns
-the chunk itself.  The hook recognises a layer of a bound PagedCache by
-the identity of the key tensor it receives and runs prefill / decode directly
-on the pages: no call re-packs the history.  With any other cache (HF's
-DynamicCache passes the whole history as key/value) the hook packs that history
-into a temporary paged cache per call -- correct, but it rewrites the whole
-context every call, so long contexts should use PagedCache.
+the chunk itself.  The hook recognises a layer of any live PagedCache by the
+identity of the key tensor it receives and runs prefill / decode directly on
+the pages: no call re-packs the history.  Since update() returns only the new
+chunk, a PagedCache must be read by this hook alone: an update that no hook
+call consumed (another attention implementation read the layer, or the key
+reached the hook as a copy) makes the next call on that layer raise instead of
+attending to the chunk only, and unregister() closes the caches of the hook it
+removes.  With any other cache (HF's DynamicCache passes the whole history as
+key/value) the hook packs that history into a temporary paged cache per call --
+correct, but it rewrites the whole context every call (a warning says so once
+per hook), so long contexts should use PagedCache.
 """
+import warnings
 import weakref
 
 import torch
@@ -55,6 +61,13 @@ from .model_tables import ModelWindow, window_from_config
 
 ATTN_NAME = "atf_window"
 PAGE = _lib.PAGE_SIZE
+
+# Every live PagedCache, whichever hook (or caller) made it: the hook finds the
+# layer a key tensor came from here, so a cache built directly or by another
+# hook is still read from its pages rather than taken for a plain cache.
+_CACHES = weakref.WeakSet()
+# model -> the hook register() installed on it (unregister closes its caches)
+_HOOKS = weakref.WeakKeyDictionary()
 
 
 class PagedLayer(CacheLayerMixin):
@@ -75,7 +88,7 @@ class PagedLayer(CacheLayerMixin):
                              device=owner.device)
         self.length = 0       # tokens written (every sequence of the batch has the same length)
         self.prev_length = 0  # length before the last update (the last chunk's first position)
-        self.last_key = None  # the key tensor of the last update (the hook's identity check)
+        self.last_key = None  # the key tensor of the last update until the hook reads it (identity check)
         self.is_initialized = True
 
     def lazy_initialization(self, key_states, value_states):
@@ -86,6 +99,14 @@ class PagedLayer(CacheLayerMixin):
         (K rotated at write when the cache has a RoPE table) and return them
         unchanged."""
         o = self.owner
+        if o.closed:
+            raise RuntimeError("this PagedCache was closed by atflash.hf.unregister(); other attention "
+                               "implementations cannot read it (update returns only the new tokens)")
+        if self.last_key is not None:
+            raise RuntimeError(
+                f"layer {self.layer_idx}: the previous update of this PagedCache layer was not read by the atflash "
+                "attention hook; a PagedCache returns only the new tokens from update(), so it works only with "
+                "the hook registered by atflash.hf.register()")
         B, hkv, L, d = key_states.shape
         if B != o.batch or hkv != o.num_kv_heads or d != _lib.HEAD_DIM:
             raise ValueError(f"key states {tuple(key_states.shape)} do not fit this cache "
@@ -165,10 +186,12 @@ class PagedCache(Cache):
                                        device=self.device).view(self.batch, self.pages_per_seq)
         self._pos = (None, None)   # (value, device int32 [batch] tensor), reused by every layer of a step
         self._lens = (None, None)
+        self.closed = False
         layers = []
         super().__init__(layers=layers)
         for i in range(int(config.num_hidden_layers)):
             layers.append(PagedLayer(self, i))
+        _CACHES.add(self)
 
     def start_positions(self, start: int) -> torch.Tensor:
         if self._pos[0] != start:
@@ -181,11 +204,25 @@ class PagedCache(Cache):
         return self._lens[1]
 
     def layer_of(self, layer_idx, key):
-        """The layer whose last update returned `key`, or None."""
+        """The layer whose last (unread) update returned `key`, or None."""
         if layer_idx is None or layer_idx >= len(self.layers):
             return None
         lyr = self.layers[layer_idx]
         return lyr if lyr.last_key is key else None
+
+    def pending(self, layer_idx, like=None):
+        """True when layer layer_idx holds an update that no hook call has read
+        (with `like`: one whose key has like's shape, dtype and device, as a
+        copy of it would)."""
+        if layer_idx is None or layer_idx >= len(self.layers):
+            return False
+        lk = self.layers[layer_idx].last_key
+        if lk is None:
+            return False
+        if like is None:
+            return True
+        return (isinstance(lk, torch.Tensor) and lk.shape == like.shape and lk.dtype == like.dtype
+                and lk.device == like.device)
 
 
 class IdentityRotary(nn.Module):
@@ -214,8 +251,9 @@ class WindowAttention:
         self.window = window
         self.mode = mode
         self.rope_at_load = bool(rope_at_load)
-        self._caches = weakref.WeakSet()
+        self._caches = weakref.WeakSet()  # the caches new_cache made (closed by unregister)
         self._rope = {}  # device -> fp32 (cos, sin) table, grown on demand
+        self._warned_repack = False
 
     def rope_table(self, n: int, device):
         """The (cos, sin) table for positions 0..n-1 (None without rope_at_load)."""
@@ -224,7 +262,11 @@ class WindowAttention:
         dev = torch.device(device)
         t = self._rope.get(dev)
         if t is None or t.shape[0] < n:
-            t = self.window.rope_table(max(int(n), 16), dev)
+            # grown geometrically (a decode loop on a plain cache asks for one
+            # more position per step), up to the tables' context
+            size = max(int(n), 16, 2 * (t.shape[0] if t is not None else 0))
+            size = max(int(n), min(size, self.window.n_ctx + 1))
+            t = self.window.rope_table(size, dev)
             self._rope[dev] = t
         return t
 
@@ -237,11 +279,21 @@ class WindowAttention:
         return cache
 
     def _paged_layer(self, module, key):
+        """The PagedCache layer whose update returned `key` (None for a plain
+        cache).  Raises when a PagedCache layer at this index holds an unread
+        update under another key tensor: the key reached the hook as a copy,
+        and it holds only the new tokens."""
         idx = getattr(module, "layer_idx", None)
-        for c in self._caches:
+        caches = list(_CACHES)
+        for c in caches:
             lyr = c.layer_of(idx, key)
             if lyr is not None:
                 return lyr
+        for c in caches:
+            if c.pending(idx, key):
+                raise RuntimeError(
+                    f"layer {idx}: a PagedCache layer was updated but the attention function received a different "
+                    "key tensor (a copy of the one update() returned); the hook cannot find the cached history")
         return None
 
     def __call__(self, module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kwargs):
@@ -251,6 +303,8 @@ class WindowAttention:
         scale = float(scaling) if scaling is not None else self.window.sm_scale
         windowed = self.mode == "win"
         lyr = self._paged_layer(module, key)
+        if lyr is not None:
+            lyr.last_key = None  # read: the layer's next update may proceed
         S = lyr.length if lyr is not None else key.shape[-2]
         if S - 1 > self.window.n_ctx:
             raise ValueError(f"context {S} exceeds the window tables' n_ctx {self.window.n_ctx}: rebuild them with "
@@ -271,6 +325,12 @@ class WindowAttention:
                                owner.rope_cs, _lib.LAYOUT_HALF_SPLIT)
             return o, None  # [b, L, hq, d]
         # any other cache: key/value hold the whole history [b, hkv, S, d]
+        if not self._warned_repack and S > 4096:
+            self._warned_repack = True
+            warnings.warn(f"atflash.hf: a plain KV cache ({S} tokens) is re-packed into a temporary paged cache on "
+                          "every attention call (the cache writer over the whole history, then the kernel); use "
+                          "hook.new_cache(...) as past_key_values to attend on persistent pages", RuntimeWarning,
+                          stacklevel=2)
         rt = self.rope_table(S, query.device)
         if L == 1:
             kc, vc, table = I.pack_kv(key.transpose(1, 2), value.transpose(1, 2), rope=rt)
@@ -303,6 +363,7 @@ def register(model, k_prefill: float = 2.0, k_decode: float = 2.0, n_ctx: int = 
     elif not rope_at_load and isinstance(rot, IdentityRotary):
         model.model.rotary_emb = rot.original
     AttentionInterface.register(ATTN_NAME, hook)
+    _HOOKS[model] = hook
     if hasattr(model, "set_attn_implementation"):
         model.set_attn_implementation(ATTN_NAME)
     else:
@@ -311,7 +372,14 @@ def register(model, k_prefill: float = 2.0, k_decode: float = 2.0, n_ctx: int = 
 
 
 def unregister(model, attn_implementation: str = "eager") -> None:
-    """Give the model back its own rotary embedding and the given attention."""
+    """Give the model back its own rotary embedding and the given attention.
+    Closes the PagedCaches that register()'s hook on this model made: another
+    attention implementation cannot read them, and their update() refuses
+    further tokens."""
+    hook = _HOOKS.pop(model, None)
+    if hook is not None:
+        for c in list(hook._caches):
+            c.closed = True
     rot = model.model.rotary_emb
     if isinstance(rot, IdentityRotary):
         model.model.rotary_emb = rot.original

@@ -10,6 +10,14 @@ decode   `single_decode_with_kv_cache(q, k, v, maybe_zhi=...)` as the FlashInfer
          q [Hq, 128], k/v NHD [N, Hkv, 128] or HND [Hkv, N, 128].
 paged    `prefill_paged` / `decode_paged` on a PagedKVCache, the serving path.
 
+Cost of the contiguous entry points: `_flash_attn_fwd` and
+`single_decode_with_kv_cache` take the whole history as contiguous k/v, like the
+reference's kernels, so every call first packs it into a fresh paged cache
+(`pack_kv`: an allocation and the cache writer over all Nk tokens, about 124 us
+at 128K tokens x 4 kv heads) before the attention kernel.  A decode loop should
+keep a PagedKVCache (or atflash.hf.PagedCache) and call `decode_paged`, which
+writes each token once.
+
 Differences from the reference that a caller sees:
   * prefill takes the 16-dim level table zhi; decode takes either the
     FlashInfer port's per-slice vec8 table (16 entries, per-key rule) or the
