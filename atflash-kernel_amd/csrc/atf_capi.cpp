@@ -360,7 +360,25 @@ int atf_decode_paged_bf16_noalloc(void* out, int64_t o_sb, int64_t o_sh, const v
                 "decode without allocation: %d x %d sequence x kv head pairs need %zu bytes of split partials; the "
                 "fixed scratch holds %zu (use atf_decode_paged_bf16 with a workspace)",
                 batch, num_kv_heads, partial, atf::kDecScratchBytes);
+  // The scratch used is the current device's: the stream must belong to it.
+  int dev = 0;
+  if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (stream != nullptr) {
+    hipDevice_t sdev = 0;
+    if (hipError_t e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev); e != hipSuccess)
+      return hip_fail(e, "hipStreamGetDevice");
+    if (sdev != dev)
+      return fail(ATF_ERR_INVALID,
+                  "decode without allocation: the stream belongs to device %d but device %d is current; make the "
+                  "stream's device current first",
+                  static_cast<int>(sdev), dev);
+  }
   hipError_t e = atf::launch_decode_noalloc(a, static_cast<hipStream_t>(stream));
+  if (e == hipErrorStreamCaptureUnsupported)
+    return fail(ATF_ERR_INVALID,
+                "decode without allocation: the first call on device %d was made under stream capture; make one "
+                "call on each device outside capture first (it looks up the device's scratch address)",
+                dev);
   if (e != hipSuccess) return hip_fail(e, "decode (no allocation) launch");
   return ok();
 }

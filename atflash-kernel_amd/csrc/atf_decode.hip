@@ -520,13 +520,20 @@ std::mutex g_scratch_mu;
 uint8_t* g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device, null until looked up
 
 // The current device's scratch, looked up on its first use on that device.
-hipError_t device_scratch(uint8_t** out) {
+// That first use must not be under stream capture on `s` (the lookup is not a
+// stream operation and may load the code object): it fails with
+// hipErrorStreamCaptureUnsupported instead.
+hipError_t device_scratch(uint8_t** out, hipStream_t s) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch_ptr[dev] == nullptr) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(s, &cs);
+    if (e != hipSuccess) return e;
+    if (cs != hipStreamCaptureStatusNone) return hipErrorStreamCaptureUnsupported;
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess) return e;
@@ -541,7 +548,7 @@ hipError_t device_scratch(uint8_t** out) {
 hipError_t launch_decode_noalloc(DecodeArgs a, hipStream_t s) {
   if (a.batch <= 0) return hipSuccess;
   uint8_t* base = nullptr;
-  hipError_t e = device_scratch(&base);
+  hipError_t e = device_scratch(&base, s);
   if (e != hipSuccess) return e;
   a.ws_ml = reinterpret_cast<float*>(base);
   a.ws_o = a.ws_ml + static_cast<size_t>(a.batch) * a.hkv * a.n_splits * kDecMaxGroup * 2;

@@ -31,6 +31,8 @@
 //   pre-rotated bf16 Q is used unscaled and the scale multiplies the fp32
 //   scores instead (kernel template kRaw).  O and l are rescaled only when a
 //   row's max grows past m_ref by more than 8, so P <= 256.
+#include <mutex>
+
 #include "atf_launch.h"
 
 namespace atf {
@@ -757,17 +759,33 @@ __global__ void prefill_tile_levels_kernel(int32_t* out, int n_row_tiles, int n_
   out[i] = w.advance(lt, kb >> 1);
 }
 
+namespace {
+constexpr int kPfMaxDevices = 64;
+std::mutex g_attr_mu;
+bool g_attr_set[kPfMaxDevices];  // the 160 KB dynamic-LDS attribute is set on this device
+
+// Both prefill kernels may use all 160 KB of LDS: the attribute is set once per
+// device (the current one), under a lock, before the first launch there.
+hipError_t ensure_lds_attribute() {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kPfMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_attr_mu);
+  if (g_attr_set[dev]) return hipSuccess;
+  for (const void* f : {reinterpret_cast<const void*>(prefill_kernel<false>),
+                        reinterpret_cast<const void*>(prefill_kernel<true>)}) {
+    e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kPfLdsTotal);
+    if (e != hipSuccess) return e;
+  }
+  g_attr_set[dev] = true;
+  return hipSuccess;
+}
+}  // namespace
+
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t s) {
   if (a.nq <= 0 || a.batch <= 0) return hipSuccess;
-  static bool attr_set = false;
-  if (!attr_set) {
-    for (const void* f : {reinterpret_cast<const void*>(prefill_kernel<false>),
-                          reinterpret_cast<const void*>(prefill_kernel<true>)}) {
-      hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kPfLdsTotal);
-      if (e != hipSuccess) return e;
-    }
-    attr_set = true;
-  }
+  if (hipError_t e = ensure_lds_attribute(); e != hipSuccess) return e;
   const int blocks = a.batch * a.n_qgroups * a.hq * 8;
   if (a.rope_cs != nullptr)
     hipLaunchKernelGGL(prefill_kernel<false>, dim3(blocks), dim3(kPfWaves * 64), kPfLdsTotal, s, a);

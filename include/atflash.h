@@ -181,9 +181,11 @@ int atf_decode_paged_slices_bf16(void* out, int64_t o_sb, int64_t o_sh,
  * Limit: atf_decode_workspace_bytes(...) <= 8 MiB, otherwise
  * ATF_ERR_UNSUPPORTED; the split rule keeps every request within about 4.1 MiB
  * (fewer than 512 sequence x kv head x split triples).  The first call on a
- * device looks up the array's address there; the current device must be the
- * stream's.  Every call on a GPU shares that GPU's scratch: calls that overlap
- * on one GPU (different streams, other threads) race.
+ * device looks up the array's address there, so it must be made outside stream
+ * capture (under capture it returns ATF_ERR_INVALID and launches nothing);
+ * later calls may be captured.  The current device must be the stream's
+ * (ATF_ERR_INVALID otherwise).  Every call on a GPU shares that GPU's scratch:
+ * calls that overlap on one GPU (different streams, other threads) race.
  */
 int atf_decode_paged_bf16_noalloc(void* out, int64_t o_sb, int64_t o_sh,
                                   const void* q, int64_t q_sb, int64_t q_sh,
