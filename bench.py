@@ -32,6 +32,18 @@ cpu_baseline  the oracle's fp32 banded reference (oracle/attention.py) on the
           host cores: configuration C1 (N = 2048, 4 q heads, window k = 2 and
           OFF) measured, median of 5 calls; and, as a secondary figure, the 128K
           bench prefill extrapolated from sampled 32-row query tiles.
+clocks    every timed section runs with a background thread reading the GPU's
+          metrics table (per-XCD gfx clock, socket power, hotspot temperature,
+          power-limit residency) every 20 ms; `detail.clocks` has the
+          summaries and `roofline.gfxclk_mhz` the prefill's median clock.
+decode    besides the eager back-to-back figure, every decode configuration is
+          also replayed from a HIP graph (`*_graph_us`): the GPU time without
+          the host's per-call work, which sets an eager loop's pace at short
+          contexts.
+detail    the other published configurations (Llama-3.2-3B prefill and decode,
+          Qwen2.5-7B chunked prefill to 512K and decode at 512K) and C5, one
+          whole request on the random-init 28-layer Qwen2.5-7B (256K prompt in
+          64K chunks, 64 greedy steps; window OFF, k = 2, k = 64).
 """
 import argparse
 import json
@@ -49,6 +61,116 @@ for _p in (ROOT, os.path.join(ROOT, "atflash-kernel_amd")):
 HQ, HKV, D, BASE = 28, 4, 128, 1e7
 PEAK_BF16 = 2.5e15
 PEAK_HBM = 8.0e12
+
+
+class ClockSampler:
+    """GPU clock and power while a timed section runs.
+
+    A background thread reads the device's metrics table (amdsmi
+    gpu_metrics, the SMU's own counters: per-XCD current gfx clock, socket
+    power, hotspot temperature, power-limit (PPT) residency) every `period`
+    seconds between __enter__ and __exit__.  The reference records its GPU's
+    clocks and power before and after each run (microbench/b1_bench_protocol.py:
+    69-75,110-111); sampling during the run shows the clock the kernels ran at,
+    which the part's power limit sets under MFMA load.  Where the metrics
+    cannot be read (no amdsmi, no permission) the summary says so and timing
+    is unaffected."""
+
+    _handle = None
+    _error = None
+
+    def __init__(self, period=0.02):
+        self.period = period
+        self.samples = []
+        self.first = self.last = None
+        self._stop = None
+        self._thread = None
+
+    @classmethod
+    def handle(cls):
+        if cls._handle is None and cls._error is None:
+            try:
+                import amdsmi
+                import torch
+                amdsmi.amdsmi_init()
+                hs = amdsmi.amdsmi_get_processor_handles()
+                if not hs:
+                    raise RuntimeError("no GPU handles")
+                h = hs[0]
+                if len(hs) > 1:  # pick the one torch sees as cuda:0, by PCI bus
+                    p = torch.cuda.get_device_properties(0)
+                    want = f"{getattr(p, 'pci_domain_id', 0):04x}:{p.pci_bus_id:02x}:{p.pci_device_id:02x}"
+                    for c in hs:
+                        if amdsmi.amdsmi_get_gpu_device_bdf(c).lower().startswith(want):
+                            h = c
+                            break
+                cls._handle = (amdsmi, h)
+            except Exception as e:  # noqa: BLE001 - any failure only disables the figures
+                cls._error = f"{type(e).__name__}: {e}"
+        return cls._handle
+
+    @staticmethod
+    def _num(x):
+        return x if isinstance(x, (int, float)) and not isinstance(x, bool) else None
+
+    def read(self):
+        hd = self.handle()
+        if hd is None:
+            return None
+        amdsmi, h = hd
+        try:
+            m = amdsmi.amdsmi_get_gpu_metrics_info(h)
+        except Exception:  # noqa: BLE001
+            return None
+        clks = [c for c in (m.get("current_gfxclks") or []) if self._num(c) and c > 0]
+        return {"t": time.perf_counter(),
+                "gfxclk": statistics.fmean(clks) if clks else self._num(m.get("current_gfxclk")),
+                "power": self._num(m.get("current_socket_power")),
+                "temp": self._num(m.get("temperature_hotspot")),
+                "ppt": self._num(m.get("ppt_residency_acc")),
+                "acc": self._num(m.get("accumulation_counter"))}
+
+    def _run(self):
+        while not self._stop.wait(self.period):
+            r = self.read()
+            if r is not None:
+                self.samples.append(r)
+
+    def __enter__(self):
+        import threading
+        self.first = self.read()
+        if self.first is not None:
+            self._stop = threading.Event()
+            self._thread = threading.Thread(target=self._run, daemon=True)
+            self._thread.start()
+        return self
+
+    def __exit__(self, *exc):
+        if self._thread is not None:
+            self._stop.set()
+            self._thread.join()
+        self.last = self.read()
+        return False
+
+    def summary(self):
+        if self.first is None:
+            return {"available": False, "reason": self._error or "gpu_metrics unreadable"}
+
+        def st(key):
+            xs = [r[key] for r in self.samples if r[key] is not None]
+            if not xs:
+                return None
+            return {"median": statistics.median(xs), "mean": statistics.fmean(xs), "min": min(xs), "max": max(xs)}
+        out = {"available": True, "source": "amdsmi gpu_metrics (SMU counters)", "samples": len(self.samples),
+               "period_s": self.period, "gfxclk_mhz": st("gfxclk"), "socket_power_w": st("power"),
+               "hotspot_c": st("temp"),
+               "before": {k: self.first[k] for k in ("gfxclk", "power", "temp")},
+               "after": {k: self.last[k] for k in ("gfxclk", "power", "temp")} if self.last else None}
+        if self.last and None not in (self.first["ppt"], self.last["ppt"], self.first["acc"], self.last["acc"]):
+            d_acc = self.last["acc"] - self.first["acc"]
+            if d_acc > 0:
+                out["ppt_residency"] = (self.last["ppt"] - self.first["ppt"]) / d_acc
+        return out
 
 
 def _traffic():
@@ -89,6 +211,35 @@ def _events_time_batch(fn, n):
     return s.elapsed_time(e) / n
 
 
+def _graph_time(fn, calls, reps=5):
+    """Average ms per call of `calls` calls captured in one HIP graph and
+    replayed `reps` times under one event pair: the calls' GPU time without the
+    host's per-call launch work (Python argument checks, ctypes), which at short
+    contexts takes longer than the kernels and would set an eager loop's pace."""
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(calls):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        graph.replay()
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / (reps * calls)
+    del graph
+    return ms
+
+
 def _stats(ts):
     return {"median_ms": statistics.median(ts), "mean_ms": statistics.fmean(ts), "min_ms": min(ts),
             "max_ms": max(ts), "n": len(ts)}
@@ -109,14 +260,16 @@ def bench_gpu(args):
     windows = {"off": None, "k2": AW.window_zhi_from_kret(D, BASE, 2.0, 1 << 23),
                "k64": AW.window_zhi_from_kret(D, BASE, 64.0, 1 << 23)}
     scale = 1.0 / math.sqrt(D)
-    res = {"prefill": {}, "prefill_attn": {}, "decode": {}}
+    res = {"prefill": {}, "prefill_attn": {}, "decode": {}, "clocks": {}}
 
     # ---- prefill: full op ----
     for name, zhi in (windows.items() if args.only in ("all", "prefill") else []):
         fn = lambda: interface._flash_attn_fwd(q, k, v, atflash_window_zhi=zhi, rope=rt)  # noqa: E731
         for _ in range(args.warmup):
             fn()
-        res["prefill"][name] = _stats(_events_time(fn, args.steps))
+        with ClockSampler() as cs:
+            res["prefill"][name] = _stats(_events_time(fn, args.steps))
+        res["clocks"]["prefill_" + name] = cs.summary()
         print(f"[bench] prefill {name}: {res['prefill'][name]['median_ms']:.3f} ms", flush=True)
 
     # ---- prefill attention kernel alone (roofline), on a pre-packed cache ----
@@ -126,8 +279,12 @@ def bench_gpu(args):
         fn = lambda: ops.prefill(q, kc, vc, table, N, 0, zl, scale, rt, 0)  # noqa: E731
         for _ in range(max(1, args.warmup // 2)):
             fn()
-        res["prefill_attn"][name] = _stats(_events_time(fn, args.steps))
-        print(f"[bench] prefill attention kernel {name}: {res['prefill_attn'][name]['median_ms']:.3f} ms", flush=True)
+        with ClockSampler() as cs:
+            res["prefill_attn"][name] = _stats(_events_time(fn, args.steps))
+        res["clocks"]["prefill_attn_" + name] = cs.summary()
+        clk = res["clocks"]["prefill_attn_" + name].get("gfxclk_mhz") or {}
+        print(f"[bench] prefill attention kernel {name}: {res['prefill_attn'][name]['median_ms']:.3f} ms"
+              + (f" (gfx clock median {clk['median']:.0f} MHz)" if clk else ""), flush=True)
     del kc, vc, table
 
     # ---- decode: paged cache, permuted pages, pools rotated past the MALL ----
@@ -149,7 +306,9 @@ def bench_gpu(args):
         fw = lambda: torch.ops.atflash.kv_write(caches[0].k, caches[0].v, k, v, z0, tables[0], rt, 0)  # noqa: E731
         for _ in range(args.warmup):
             fw()
-        res["kv_write"] = {"batch_mean_ms": _events_time_batch(fw, args.steps * 4)}
+        with ClockSampler() as cs:
+            res["kv_write"] = {"batch_mean_ms": _events_time_batch(fw, args.steps * 4)}
+        res["clocks"]["kv_write"] = cs.summary()
         print(f"[bench] kv_write: {res['kv_write']['batch_mean_ms'] * 1e3:.1f} us", flush=True)
     qd = torch.randn((1, HQ, D), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
     seq = torch.tensor([N], dtype=torch.int32, device=dev)
@@ -169,11 +328,16 @@ def bench_gpu(args):
             return ops.decode_paged(qd, caches[i].k, caches[i].v, tables[i], seq, N, zl, scale, rt, 0)
         for _ in range(args.warmup * 10):
             fn()
-        res["decode"][name] = _stats(_events_time(fn, args.steps * 40))
-        # per-launch average over a batch with no event packets between launches:
-        # the figure the roofline uses (it matches the kernel trace's average)
-        res["decode"][name]["batch_mean_ms"] = _events_time_batch(fn, args.steps * 40)
-        print(f"[bench] decode {name}: {res['decode'][name]['median_ms'] * 1e3:.2f} us", flush=True)
+        with ClockSampler() as cs:
+            res["decode"][name] = _stats(_events_time(fn, args.steps * 40))
+            # per-launch average over a batch with no event packets between launches:
+            # the figure the roofline uses (it matches the kernel trace's average)
+            res["decode"][name]["batch_mean_ms"] = _events_time_batch(fn, args.steps * 40)
+        res["clocks"]["decode_" + name] = cs.summary()
+        # the same calls replayed from a HIP graph (no host launch work)
+        res["decode"][name]["graph_mean_ms"] = _graph_time(fn, 8 * copies)
+        print(f"[bench] decode {name}: {res['decode'][name]['batch_mean_ms'] * 1e3:.2f} us per call "
+              f"(graph replay {res['decode'][name]['graph_mean_ms'] * 1e3:.2f} us)", flush=True)
     res["decode_pool_bytes"] = copies * n_pages * HKV * 8192
     return res
 
@@ -271,12 +435,15 @@ def bench_detail(steps=3):
                 for _ in range(10):
                     fn()
                 r[name + "_us"] = _events_time_batch(fn, 40 * steps) * 1e3
+                r[name + "_graph_us"] = _graph_time(fn, 8 * copies) * 1e3
             r["on_over_off"] = r["off_us"] / r["k2_us"]
+            r["on_over_off_graph"] = r["off_graph_us"] / r["k2_graph_us"]
             if B == 1:
                 r.update(_ref_ratio("llama_decode_b1_us", N))
             out["llama_decode"][f"b{B}_{N}"] = r
             print(f"[bench detail] llama decode B={B} {N}: off {r['off_us']:.1f} us k2 {r['k2_us']:.1f} us "
-                  f"({r['on_over_off']:.3f}x" + (f"; reference {r['reference_ratio']:.3f}x)" if B == 1 else ")"),
+                  f"({r['on_over_off']:.3f}x; graph replay off {r['off_graph_us']:.1f} k2 {r['k2_graph_us']:.1f} us, "
+                  f"{r['on_over_off_graph']:.3f}x" + (f"; reference {r['reference_ratio']:.3f}x)" if B == 1 else ")"),
                   flush=True)
             del pool, tables, q, rt
             torch.cuda.empty_cache()
@@ -329,6 +496,7 @@ def bench_detail(steps=3):
         for _ in range(10):
             fn()
         r[name + "_us"] = _events_time_batch(fn, 20 * steps) * 1e3
+        r[name + "_graph_us"] = _graph_time(fn, 8) * 1e3
     r["on_over_off"] = r["off_us"] / r["k2_us"]
     r["on_over_off_vec8"] = r["off_us"] / r["k2_vec8_us"]
     r["off_frac_of_8TBs"] = N * HKV * D * 2 * 2 / (r["off_us"] * 1e-6) / PEAK_HBM
@@ -338,6 +506,76 @@ def bench_detail(steps=3):
     del pool, tab, q, rt
     torch.cuda.empty_cache()
     return out
+
+
+# The reference's published whole-request speedups of its e2e harness (RTX PRO
+# 6000, real Qwen2.5-7B-Instruct-1M weights): k = 2 at 256K 1.17x (README.md:76),
+# k = 64 at 256K 1.09x (e2e_pipeline/README.md:42-43), k = 2 at 1M 1.31x.
+REF_E2E = {"k2": 1.17, "k64": 1.09}
+
+
+def bench_c5(tokens=262144, chunk=65536, steps=64):
+    """Configuration C5: one request on the random-init Qwen2.5-7B architecture
+    (28 layers, bf16) through the HF hook and the paged cache -- a chunked
+    prefill of `tokens` uniform-random prompt ids in `chunk`-token chunks, then
+    `steps` greedy decode steps -- window OFF, k = 2 and k = 64, timed as the
+    reference's harness times it (atflash.e2e.run_request: HIP events around the
+    prefill and each step, wall clock around the request)."""
+    import gc
+    import torch
+    from atflash import e2e
+    from atflash.model_tables import WIN_ZHI_CAP
+    dev = torch.device("cuda:0")
+    t0 = time.perf_counter()
+    cfg = e2e.qwen25_7b_config()
+    model = e2e.build_model(cfg, dev, seed=0)
+    g = torch.Generator(device=dev).manual_seed(1)
+    ids = torch.randint(0, cfg.vocab_size, (1, tokens), generator=g, device=dev)
+    warm = e2e.use_mode(model, "off", WIN_ZHI_CAP)
+    e2e.run_request(model, warm, ids[:, :min(tokens, 2 * chunk)], chunk, 2)
+    print(f"[bench c5] model built and warmed in {time.perf_counter() - t0:.1f} s", flush=True)
+    out = {"workload": f"random-init Qwen2.5-7B (28 layers, bf16), {tokens}-token prompt in {chunk}-token chunks, "
+                       f"{steps} greedy steps", "tokens": tokens, "chunk": chunk, "steps": steps, "modes": {}}
+    for mode in ("off", "k2", "k64"):
+        hook = e2e.use_mode(model, mode, WIN_ZHI_CAP)
+        with ClockSampler(period=0.1) as cs:
+            r = e2e.run_request(model, hook, ids, chunk, steps, progress=f"c5 {mode}")
+        r.pop("step_ms")
+        r["tokens_out"] = r.pop("tokens")
+        r["clock"] = cs.summary()
+        out["modes"][mode] = r
+        print(f"[bench c5] {mode}: prefill {r['prefill_ms']:.0f} ms, {steps} steps {r['decode_ms_total']:.0f} ms, "
+              f"request {r['wall_s']:.2f} s", flush=True)
+        torch.cuda.empty_cache()
+    off = out["modes"]["off"]
+    for mode in ("k2", "k64"):
+        m = out["modes"][mode]
+        m["request_speedup"] = off["wall_s"] / m["wall_s"]
+        m["prefill_speedup"] = off["prefill_ms"] / m["prefill_ms"]
+        m["decode_speedup"] = off["decode_ms_total"] / m["decode_ms_total"]
+        m["reference_request_speedup"] = REF_E2E[mode]
+    del model, warm, hook, ids
+    gc.collect()
+    torch.cuda.empty_cache()
+    return out
+
+
+PEAK_CLOCK_MHZ = 2400.0  # the shader clock the 2.5 PFLOP/s bf16 peak is quoted at
+
+
+def _clk(summary):
+    """Median gfx clock (MHz) of a timed section, or None."""
+    try:
+        return summary["gfxclk_mhz"]["median"]
+    except (TypeError, KeyError):
+        return None
+
+
+def _frac_at_clock(frac, summary):
+    """A fraction of the 2.5 PFLOP/s peak restated against the peak at the
+    clock the section actually ran at (peak scales with the clock)."""
+    c = _clk(summary)
+    return None if not c else frac * PEAK_CLOCK_MHZ / c
 
 
 def slice_ratios(N):
@@ -428,6 +666,7 @@ def main():
     ap.add_argument("--n", type=int, default=131072)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-detail", action="store_true", help="skip the other published configurations")
+    ap.add_argument("--no-c5", action="store_true", help="skip the end-to-end request (configuration C5)")
     ap.add_argument("--only", choices=("all", "prefill", "decode", "kv_write", "copy"), default="all",
                     help="run one workload (for profiler runs); 'copy' is a plain 1 GiB device copy "
                          "used to calibrate the FETCH_SIZE / WRITE_SIZE counters")
@@ -463,6 +702,7 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_wall
     detail_cfgs = None if args.no_detail else bench_detail()
+    c5 = None if (args.no_detail or args.no_c5) else bench_c5()
     sr = slice_ratios(N)
 
     flops_off = 2.0 * HQ * N * N * D
@@ -482,8 +722,9 @@ def main():
             s = sr[name]["s_decode"]
         nbytes = N * HKV * D * 2 * (1.0 + s) + HQ * D * 4
         t = res["decode"][name]["batch_mean_ms"] * 1e-3
+        tg = res["decode"][name]["graph_mean_ms"] * 1e-3
         dec[name] = {"bytes": nbytes, "GBps": nbytes / t / 1e9, "frac": nbytes / t / PEAK_HBM,
-                     "us_per_launch": t * 1e6}
+                     "us_per_launch": t * 1e6, "us_per_launch_graph": tg * 1e6, "frac_graph": nbytes / tg / PEAK_HBM}
 
     # KV-cache writer: K and V read once and written once, plus the RoPE table
     # row (64 (cos, sin) fp32 pairs) of each position once
@@ -526,6 +767,9 @@ def main():
         "roofline": {"bound": "mfma", "achieved": roof["off"]["tflops"], "peak": PEAK_BF16 / 1e12,
                      "unit": "TFLOP/s", "frac": roof["off"]["frac"], "traffic": roof["off"]["traffic"],
                      "kernel": "atf::prefill_kernel, window OFF",
+                     "gfxclk_mhz": _clk(res["clocks"].get("prefill_attn_off")),
+                     "frac_of_peak_at_measured_clock": _frac_at_clock(roof["off"]["frac"],
+                                                                      res["clocks"].get("prefill_attn_off")),
                      "per_window": roof},
         "roofline_decode": {"bound": "hbm", "achieved": dec["off"]["GBps"], "peak": PEAK_HBM / 1e9,
                             "unit": "GB/s", "frac": dec["off"]["frac"], "traffic": dec["off"]["traffic"],
@@ -539,20 +783,26 @@ def main():
             "prefill_attn_kernel_ms": {n: attn[n]["median_ms"] for n in attn},
             "decode_us": {n: res["decode"][n]["batch_mean_ms"] * 1e3 for n in res["decode"]},
             "decode_us_per_call_median": {n: res["decode"][n]["median_ms"] * 1e3 for n in res["decode"]},
+            "decode_us_graph": {n: res["decode"][n]["graph_mean_ms"] * 1e3 for n in res["decode"]},
             "prefill_on_over_off": {n: pre["off"]["median_ms"] / pre[n]["median_ms"] for n in ("k2", "k64")},
             "decode_on_over_off": {n: res["decode"]["off"]["batch_mean_ms"] / res["decode"][n]["batch_mean_ms"]
                                    for n in res["decode"] if n != "off"},
+            "decode_on_over_off_graph": {n: res["decode"]["off"]["graph_mean_ms"] / res["decode"][n]["graph_mean_ms"]
+                                         for n in res["decode"] if n != "off"},
+            "clocks": res["clocks"],
             "slice_ratios": sr,
             "ceilings": {n: {"prefill": 2 / (1 + sr[n]["s_prefill"]), "decode": 2 / (1 + sr[n]["s_decode"]),
                              "decode_vec8": 2 / (1 + sr[n]["s_decode_vec8"])} for n in sr},
             "kv_write_us": kvw["us_per_launch"],
             "decode_pool_bytes": res["decode_pool_bytes"],
             "timed_region_wall_s": wall,
-            "stats": res,
+            "stats": {k: v for k, v in res.items() if k != "clocks"},
         },
     }
     if detail_cfgs is not None:
         line["detail"]["configs"] = detail_cfgs
+    if c5 is not None:
+        line["detail"]["configs"]["c5"] = c5
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(N)
     print(json.dumps(line))
