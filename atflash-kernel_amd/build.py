@@ -29,13 +29,20 @@ COMMON = [
 ]
 
 
+# Per-file flags.  The decode kernels take their first arguments as scalars
+# that the dispatch preloads into SGPRs (kernarg preloading, gfx950): up to 14
+# dwords (16 user SGPRs less the argument-block pointer).  A firmware without
+# it runs the compiler's compatibility prologue, which loads them instead.
+EXTRA = {"atf_decode.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=14"]}
+
+
 def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith((".hip", ".cpp")))
 
 
 def compile_one(src):
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *COMMON, "-I", CSRC, "-c", src, "-o", obj]
+    cmd = [HIPCC, *COMMON, *EXTRA.get(os.path.basename(src), []), "-I", CSRC, "-c", src, "-o", obj]
     p = subprocess.run(cmd, capture_output=True, text=True)
     if p.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{p.stderr}")

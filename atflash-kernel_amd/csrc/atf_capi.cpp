@@ -99,13 +99,22 @@ int check_layout(int layout, const float* rope_cs, int rope_max_pos) {
   return ATF_OK;
 }
 
-void decode_split(int batch, int hkv, int max_seq_len, int* n_splits, int* pages_per_split) {
+void decode_split(int batch, int hkv, int max_seq_len, int* n_splits, int* pages_per_split, int* waves) {
   const int pages = max_seq_len > 0 ? (max_seq_len + atf::kPage - 1) / atf::kPage : 1;
-  // one workgroup (8 waves) per CU over 256 CUs; at least one 4-page group per wave
+  // one workgroup per CU over 256 CUs; at least one 4-page group per wave.
+  // Workgroups of 8 waves, unless their 32-page minimum leaves fewer splits
+  // than the target while there are several anyway: then 4 waves, whose
+  // 16-page minimum spreads the context over up to twice as many CUs
+  // (Llama-3.2-3B shape at 8K: 128 -> 256 workgroups, -12% per call).  A
+  // context that fits one 8-wave split keeps it (a second split would add the
+  // merge kernel).
   const int target_wgs = 256;
-  const int min_pps = atf::kDecUnroll * atf::kDecWaves;
   int ns = (target_wgs + batch * hkv - 1) / (batch * hkv);
   if (ns < 1) ns = 1;
+  const int splits8 = (pages + atf::kDecUnroll * atf::kDecWaves - 1) / (atf::kDecUnroll * atf::kDecWaves);
+  const int w = (splits8 < ns && splits8 >= 2) ? atf::kDecWavesShort : atf::kDecWaves;
+  const int min_pps = atf::kDecUnroll * w;
+  *waves = w;
   int pps = (pages + ns - 1) / ns;
   if (pps < min_pps) pps = min_pps;
   if ((pages + pps - 1) / pps > atf::kDecMaxSplits) pps = (pages + atf::kDecMaxSplits - 1) / atf::kDecMaxSplits;
@@ -223,8 +232,8 @@ int atf_prefill_bf16(void* out, int64_t o_sb, int64_t o_st, int64_t o_sh, float*
 size_t atf_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int max_seq_len) {
   (void)num_q_heads;
   if (batch <= 0 || num_kv_heads <= 0) return 0;
-  int ns = 1, pps = 1;
-  decode_split(batch, num_kv_heads, max_seq_len, &ns, &pps);
+  int ns = 1, pps = 1, waves = 0;
+  decode_split(batch, num_kv_heads, max_seq_len, &ns, &pps, &waves);
   return partial_bytes(batch, num_kv_heads, ns);
 }
 
@@ -260,8 +269,9 @@ int decode_prepare(void* out, int64_t o_sb, int64_t o_sh, const void* q, int64_t
   if (int r = slice_table ? make_decode_table_slices(zhi, a)
                           : make_decode_table_levels(zhi, a, static_cast<int64_t>(max_seq_len) - 1))
     return r;
-  int ns = 1, pps = 1;
-  decode_split(batch, num_kv_heads, max_seq_len, &ns, &pps);
+  int ns = 1, pps = 1, waves = 0;
+  decode_split(batch, num_kv_heads, max_seq_len, &ns, &pps, &waves);
+  a->waves = waves;
   a->q = static_cast<const uint16_t*>(q);
   a->q_sb = q_sb;
   a->q_sh = q_sh;
@@ -380,6 +390,13 @@ int atf_decode_paged_bf16_noalloc(void* out, int64_t o_sb, int64_t o_sh, const v
                 "call on each device outside capture first (it looks up the device's scratch address)",
                 dev);
   if (e != hipSuccess) return hip_fail(e, "decode (no allocation) launch");
+  return ok();
+}
+
+int atf_prefill_mfma_probe(float* sink, int nq, int num_q_heads, void* stream) {
+  if (!sink || nq <= 0 || nq >= (1 << 24) || num_q_heads <= 0) return fail(ATF_ERR_INVALID, "bad arguments");
+  hipError_t e = atf::launch_prefill_mfma_probe(sink, nq, num_q_heads, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "probe launch");
   return ok();
 }
 

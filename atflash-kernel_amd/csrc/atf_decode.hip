@@ -65,10 +65,21 @@ struct PageRegs {
 // compiler wait for every outstanding load before the register's next use.
 // A wave fetches a page's entry one stride ahead of its use, so the page loads
 // are issued without waiting for the table.
-__device__ __forceinline__ int dec_fetch_entry(const DecodeArgs& a, int b, int p, int p_begin, int p_end) {
-  const int* row = a.page_table + static_cast<int64_t>(b) * a.max_pages;
+__device__ __forceinline__ int dec_fetch_entry(const int32_t* row, int p, int p_begin, int p_end) {
   return row[max(p_begin, min(p, p_end - 1))];
 }
+
+// The fields of the call that the first page loads need, passed as leading
+// scalar kernel arguments so that they arrive preloaded in SGPRs (kernarg
+// preloading): the page-table and sequence-length loads are issued without
+// first waiting for the argument block to be read from memory.
+struct DecHot {
+  const int32_t* page_table;
+  const int32_t* seq_lens;
+  const uint16_t* k_cache;
+  const uint16_t* v_cache;
+  int max_pages, pages_per_split, max_seq_len, hkv, num_pages;
+};
 
 // Slice count of a key at a fixed offset in its page as the page index p walks
 // up (per-slice table, per-key rule): slice s is read from page
@@ -115,7 +126,7 @@ __device__ __forceinline__ void page_slices(const DecodeArgs& a, SliceWalker& yo
 
 // K and V operands of page p whose page-table entry is `raw`, reading its first
 // ns slices of K; a page outside the split (in_split false) reads nothing.
-__device__ __forceinline__ void dec_load_page(const DecodeArgs& a, int h, int raw, bool in_split, int p, int ns,
+__device__ __forceinline__ void dec_load_page(const DecHot& a, int h, int raw, bool in_split, int p, int ns,
                                               bool mask, int lane, PageRegs& r) {
   r.n0 = p * kPage;
   r.mask = mask;
@@ -152,35 +163,37 @@ __device__ __forceinline__ void dec_load_page(const DecodeArgs& a, int h, int ra
     r.v[db] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rv, voff + db * 512u, 0, kLoadStream));
 }
 
-// two waves per SIMD: at most 256 registers per wave
-template <bool kPerKey>
-__global__ __launch_bounds__(kDecWaves * 64) __attribute__((amdgpu_waves_per_eu(2)))
-void decode_kernel(DecodeArgs a) {
+// two waves per SIMD: at most 256 registers per wave.  kWaves = 8 (one
+// workgroup per CU) or 4 (short contexts: smaller splits over more CUs).
+template <bool kPerKey, int kWaves>
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2)))
+void decode_kernel(const int32_t* page_table, const int32_t* seq_lens, const uint16_t* k_cache,
+                   const uint16_t* v_cache, int max_pages, int pages_per_split, int max_seq_len, int hkv,
+                   int num_pages, DecodeArgs a) {
+  const DecHot hot{page_table, seq_lens, k_cache, v_cache, max_pages, pages_per_split, max_seq_len, hkv, num_pages};
   // wave partials
-  __shared__ __attribute__((aligned(16))) float sh_o[kDecWaves * kDecMaxGroup * kD];
-  __shared__ float sh_m[kDecWaves * kDecMaxGroup], sh_l[kDecWaves * kDecMaxGroup];
+  __shared__ __attribute__((aligned(16))) float sh_o[kWaves * kDecMaxGroup * kD];
+  __shared__ float sh_m[kWaves * kDecMaxGroup], sh_l[kWaves * kDecMaxGroup];
 
   const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int g = lane & 15;
-  const int p_begin = s * a.pages_per_split;
-  // wave w takes the groups of kDecUnroll pages that start at p_begin + kDecUnroll * (w + kDecWaves * i).
-  constexpr int kStride = kDecUnroll * kDecWaves;
+  const int p_begin = s * hot.pages_per_split;
+  // wave w takes the groups of kDecUnroll pages that start at p_begin + kDecUnroll * (w + kWaves * i).
+  constexpr int kStride = kDecUnroll * kWaves;
   const int p_first = p_begin + kDecUnroll * __builtin_amdgcn_readfirstlane(wave);
   // The first group's page-table entries are fetched together with the
   // sequence length, their index clamped into the table row only (an entry
   // past the split is never used), so the first page loads wait for two
   // memory round trips after the kernel arguments, not three.
   int ent[kDecUnroll];
-  {
-    const int* row = a.page_table + static_cast<int64_t>(b) * a.max_pages;
+  const int32_t* row = hot.page_table + static_cast<int64_t>(b) * hot.max_pages;
 #pragma unroll
-    for (int u = 0; u < kDecUnroll; ++u) ent[u] = row[min(p_first + u, a.max_pages - 1)];
-  }
-  const int N = max(0, min(a.seq_lens[b], a.max_seq_len));
+  for (int u = 0; u < kDecUnroll; ++u) ent[u] = row[min(p_first + u, hot.max_pages - 1)];
+  const int N = max(0, min(hot.seq_lens[b], hot.max_seq_len));
   const int n_pages = (N + kPage - 1) / kPage;
-  const int p_end = min(n_pages, p_begin + a.pages_per_split);
+  const int p_end = min(n_pages, p_begin + hot.pages_per_split);
   const float NEG_INF = -__builtin_huge_valf();
   const float c = a.scale_log2;
 
@@ -209,10 +222,10 @@ void decode_kernel(DecodeArgs a) {
     int ns;
     bool mask;
     page_slices<kPerKey>(a, wy, wo, p_first + u, N, ns, mask);
-    dec_load_page(a, h, ent[u], p_first + u < p_end, p_first + u, ns, mask, lane, pr[u]);
+    dec_load_page(hot, h, ent[u], p_first + u < p_end, p_first + u, ns, mask, lane, pr[u]);
   }
 #pragma unroll
-  for (int u = 0; u < kDecUnroll; ++u) ent[u] = dec_fetch_entry(a, b, p_first + kStride + u, p_begin, p_end);
+  for (int u = 0; u < kDecUnroll; ++u) ent[u] = dec_fetch_entry(row, p_first + kStride + u, p_begin, p_end);
 
   // ---- Q^T fragments: lane holds q head g, slice 4 lp + lane/16 ----
   u32x4 Qf[4];
@@ -322,8 +335,8 @@ void decode_kernel(DecodeArgs a) {
         int ns;
         bool mask;
         page_slices<kPerKey>(a, wy, wo, pn, N, ns, mask);
-        dec_load_page(a, h, ent[u], true, pn, ns, mask, lane, pr[u]);
-        ent[u] = dec_fetch_entry(a, b, pn + kStride, p_begin, p_end);
+        dec_load_page(hot, h, ent[u], true, pn, ns, mask, lane, pr[u]);
+        ent[u] = dec_fetch_entry(row, pn + kStride, p_begin, p_end);
       }
     }
   }
@@ -342,19 +355,18 @@ void decode_kernel(DecodeArgs a) {
     }
   }
   __syncthreads();
-  // thread t owns query head t / 32, dims 4 (t % 32) .. +3 (group <= 16: 512 tasks)
-  const int gq = tid >> 5, d4 = 4 * (tid & 31);
-  const bool owner = gq < a.group;
-  const int64_t pbase = (static_cast<int64_t>(b) * a.hkv + h) * a.n_splits * kDecMaxGroup;  // split 0, head 0
-  if (owner) {
+  // thread t owns query heads t / 32 + 2 kWaves j, dims 4 (t % 32) .. +3
+  const int d4 = 4 * (tid & 31);
+  const int64_t pbase = (static_cast<int64_t>(b) * hot.hkv + h) * a.n_splits * kDecMaxGroup;  // split 0, head 0
+  for (int gq = tid >> 5; gq < a.group; gq += 2 * kWaves) {
     float M = NEG_INF;
 #pragma unroll
-    for (int w = 0; w < kDecWaves; ++w) M = fmaxf(M, sh_m[w * kDecMaxGroup + gq]);
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sh_m[w * kDecMaxGroup + gq]);
     float L = 0.f;
     f32x4 acc = f32x4{};
     if (M != NEG_INF) {
 #pragma unroll
-      for (int w = 0; w < kDecWaves; ++w) {
+      for (int w = 0; w < kWaves; ++w) {
         const float wt = fast_exp2((sh_m[w * kDecMaxGroup + gq] - M) * c);  // empty wave: m = -inf -> 0
         L += wt * sh_l[w * kDecMaxGroup + gq];
         acc += wt * *reinterpret_cast<const f32x4*>(&sh_o[(w * kDecMaxGroup + gq) * kD + d4]);
@@ -390,10 +402,9 @@ void decode_kernel(DecodeArgs a) {
 constexpr int kMergeChunks = 4;
 constexpr int kMergeDims = kD / kMergeChunks;  // 32
 
-// The merge kernel's arguments: a block of its own, every field used before
-// the first branch, so the kernel reads them in one memory round trip (with
-// the decode kernel's argument block, the fields read behind branches cost a
-// second dependent round trip before the partials could be requested).
+// The merge kernel's arguments are scalars (14 dwords), preloaded into SGPRs
+// with the dispatch, so the partial loads are issued at once instead of after
+// a read of an argument block.
 struct MergeArgs {
   const float* ws_ml;
   const float* ws_o;
@@ -420,7 +431,10 @@ __device__ __forceinline__ void merge_xor(float& m, float& l, f32x4& o, int mask
   }
 }
 
-__global__ __launch_bounds__(512) void decode_merge_kernel(MergeArgs a) {
+__global__ __launch_bounds__(512) void decode_merge_kernel(const float* ws_ml, const float* ws_o, uint16_t* out,
+                                                            int64_t o_sb, int64_t o_sh, int n_splits, int group,
+                                                            int hkv, float scale_log2) {
+  const MergeArgs a{ws_ml, ws_o, out, o_sb, o_sh, n_splits, group, hkv, scale_log2};
   const int chunk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x;
   const float NEG_INF = -__builtin_huge_valf();
@@ -496,14 +510,21 @@ __global__ void decode_page_levels_kernel(int32_t* out, int n_pages, int N, Leve
 
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t s) {
   if (a.batch <= 0) return hipSuccess;
-  if (a.per_key)
-    hipLaunchKernelGGL(decode_kernel<true>, dim3(a.n_splits, a.hkv, a.batch), dim3(kDecWaves * 64), 0, s, a);
-  else
-    hipLaunchKernelGGL(decode_kernel<false>, dim3(a.n_splits, a.hkv, a.batch), dim3(kDecWaves * 64), 0, s, a);
+  const dim3 grid(a.n_splits, a.hkv, a.batch);
+#define ATF_DEC_LAUNCH(PK, W)                                                                                   \
+  hipLaunchKernelGGL((decode_kernel<PK, W>), grid, dim3(W * 64), 0, s, a.page_table, a.seq_lens, a.k_cache,     \
+                     a.v_cache, a.max_pages, a.pages_per_split, a.max_seq_len, a.hkv, a.num_pages, a)
+  if (a.waves == 8) {
+    if (a.per_key) ATF_DEC_LAUNCH(true, 8); else ATF_DEC_LAUNCH(false, 8);
+  } else {
+    if (a.per_key) ATF_DEC_LAUNCH(true, 4); else ATF_DEC_LAUNCH(false, 4);
+  }
+#undef ATF_DEC_LAUNCH
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.n_splits == 1) return e;
-  const MergeArgs m{a.ws_ml, a.ws_o, a.out, a.o_sb, a.o_sh, a.n_splits, a.group, a.hkv, a.scale_log2};
-  hipLaunchKernelGGL(decode_merge_kernel, dim3(kMergeChunks, a.hkv, a.batch), dim3(512), 0, s, m);
+  hipLaunchKernelGGL(decode_merge_kernel, dim3(kMergeChunks, a.hkv, a.batch), dim3(512), 0, s,
+                     static_cast<const float*>(a.ws_ml), static_cast<const float*>(a.ws_o), a.out, a.o_sb, a.o_sh,
+                     a.n_splits, a.group, a.hkv, a.scale_log2);
   return hipGetLastError();
 }
 

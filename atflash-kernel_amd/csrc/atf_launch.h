@@ -18,6 +18,7 @@ constexpr int kPfWinN = 32;
 constexpr int kDecMaxGroup = 16;
 constexpr int kDecUnroll = 4;      // pages in flight per wave
 constexpr int kDecWaves = 8;       // waves per workgroup (one split), 2 per SIMD
+constexpr int kDecWavesShort = 4;  // the same for contexts too short to give 256 splits of 8 waves
 constexpr int kDecMaxSplits = 256;
 // Fixed device scratch of the entry point that allocates nothing
 // (atf_decode_paged_bf16_noalloc): split partials, laid out as in a workspace.
@@ -73,6 +74,7 @@ struct DecodeArgs {
   int max_seq_len;
   int batch, hq, hkv, group;
   int n_splits, pages_per_split;
+  int waves;  // kDecWaves or kDecWavesShort per workgroup
   float scale_log2;
   const float* rope_cs;
   int layout;
@@ -89,6 +91,9 @@ struct DecodeArgs {
 
 hipError_t launch_kv_write(const KvWriteArgs& a, hipStream_t s);
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t s);
+// The MFMA-ceiling probe of the prefill (measurement only): sink holds
+// ceil(ceil(nq / 256) / 8) * 8 * hq * 512 floats.
+hipError_t launch_prefill_mfma_probe(float* sink, int nq, int hq, hipStream_t s);
 hipError_t launch_prefill_tile_levels(int32_t* out, int n_row_tiles, int n_kblocks, int q_offset,
                                       const LevelTable& lt, hipStream_t s);
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t s);
