@@ -56,6 +56,7 @@ SIGNATURES = {
                                           _i, _i, _i, _i, _p, _f, _p, _i, _i, _p, _sz, _p]),
     "atf_decode_paged_bf16_noalloc": (_i, [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i, _p, _i, _p,
                                            _i, _i, _i, _i, _p, _f, _p, _i, _i, _p]),
+    "atf_prefill_mfma_probe": (_i, [_p, _i, _i, _p]),
     "atf_prefill_tile_levels": (_i, [_p, _i, _i, _i, _p, _p]),
     "atf_decode_page_levels": (_i, [_p, _i, _i, _p, _p]),
 }
@@ -110,14 +111,15 @@ def zhi_array(zhi, n=LEVELS):
     loop does not rebuild one per call."""
     if zhi is None:
         return None
-    vals = tuple(int(x) for x in (zhi.tolist() if isinstance(zhi, torch.Tensor) else zhi))
-    if len(vals) != n:
-        raise ValueError(f"window table must have {n} entries (head_dim / {HEAD_DIM // n}), got {len(vals)}")
-    arr = _ZHI_ARRAYS.get(vals)
+    key = tuple(zhi.tolist()) if isinstance(zhi, torch.Tensor) else tuple(zhi)
+    arr = _ZHI_ARRAYS.get((n, key))
     if arr is None:
+        vals = tuple(int(x) for x in key)
+        if len(vals) != n:
+            raise ValueError(f"window table must have {n} entries (head_dim / {HEAD_DIM // n}), got {len(vals)}")
         if len(_ZHI_ARRAYS) >= 256:
             _ZHI_ARRAYS.clear()
-        arr = _ZHI_ARRAYS[vals] = (ctypes.c_int32 * n)(*vals)
+        arr = _ZHI_ARRAYS[(n, key)] = (ctypes.c_int32 * n)(*vals)
     return arr
 
 
@@ -125,8 +127,16 @@ K_BLOCK_SHAPE = (SLICES, PAGE_SIZE, SLICE_DIMS)  # one (page, kv head) K block o
 
 
 def ptr(t):
-    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+    """Device address of a tensor as an int (None for an absent tensor): the
+    bound argument types convert it, which costs less than a c_void_p object."""
+    return t.data_ptr() if t is not None else None
+
+
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
 def stream_of(device):
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    """The current HIP stream of a device, as an int handle."""
+    if _RAW_STREAM is not None and device.index is not None:
+        return _RAW_STREAM(device.index)
+    return torch.cuda.current_stream(device).cuda_stream

@@ -128,14 +128,23 @@ def _(q, k_cache, v_cache, page_table, nk, q_offset, zhi, sm_scale, rope_cs, lay
 # needs no initialisation (each call writes the split partials it reads), and
 # calls on one stream are ordered, so they can share it.
 _DECODE_WS = {}
+_WS_BYTES = {}  # (batch, hq, hkv, max_seq_len) -> workspace bytes the split rule needs
 
 
-def _decode_workspace(device, handle, nbytes):
+def _decode_workspace(device, handle, B, hq, hkv, max_seq_len, L):
+    """(address, bytes) of the workspace of (device, stream), grown to what a
+    call of this shape needs."""
+    shape = (B, hq, hkv, max_seq_len)
+    nbytes = _WS_BYTES.get(shape)
+    if nbytes is None:
+        if len(_WS_BYTES) >= 4096:
+            _WS_BYTES.clear()
+        nbytes = _WS_BYTES[shape] = int(L.atf_decode_workspace_bytes(B, hq, hkv, max_seq_len))
     key = (device.index, handle)
     ws = _DECODE_WS.get(key)
-    if ws is None or ws.numel() * 4 < nbytes:
-        ws = torch.empty((max(nbytes, 16) + 3) // 4, dtype=torch.float32, device=device)
-        _DECODE_WS[key] = ws
+    if ws is None or ws[1] < nbytes:
+        t = torch.empty((max(nbytes, 16) + 3) // 4, dtype=torch.float32, device=device)
+        ws = _DECODE_WS[key] = (t.data_ptr(), t.numel() * 4, t)
     return ws
 
 
@@ -150,26 +159,29 @@ def decode_paged(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
     _check_cache(k_cache, v_cache)
     _need(q.dtype == torch.bfloat16 and q.dim() == 3 and q.shape[-1] == _lib.HEAD_DIM,
           "q must be bf16 [B, Hq, 128]")
-    _need(q.stride(-1) == 1, "last dim of q must be contiguous")
-    _need(seq_lens.dtype == torch.int32 and seq_lens.numel() == q.shape[0], "seq_lens must be int32 [B]")
-    _need(page_table.dtype == torch.int32 and page_table.dim() == 2 and page_table.shape[0] == q.shape[0]
-          and page_table.is_contiguous(), "page_table must be contiguous int32 [B, max_pages]")
+    q_sb, q_sh, q_sd = q.stride()
+    _need(q_sd == 1, "last dim of q must be contiguous")
     B, Hq, _ = q.shape
-    hkv = k_cache.shape[1]
+    _need(seq_lens.dtype == torch.int32 and seq_lens.numel() == B, "seq_lens must be int32 [B]")
+    _need(page_table.dtype == torch.int32 and page_table.dim() == 2 and page_table.shape[0] == B
+          and page_table.is_contiguous(), "page_table must be contiguous int32 [B, max_pages]")
+    num_pages, hkv = k_cache.shape[0], k_cache.shape[1]
     rope_cs, max_pos = _rope(rope_cs)
     L = _lib.lib()
-    nbytes = int(L.atf_decode_workspace_bytes(B, Hq, hkv, int(max_seq_len)))
-    stream = _lib.stream_of(q.device)
-    ws = _decode_workspace(q.device, stream.value, nbytes)
-    out = torch.empty((B, Hq, _lib.HEAD_DIM), dtype=torch.bfloat16, device=q.device)
+    dev = q.device
+    stream = _lib.stream_of(dev)
+    ws = _decode_workspace(dev, stream, B, Hq, hkv, int(max_seq_len), L)
+    out = torch.empty((B, Hq, _lib.HEAD_DIM), dtype=torch.bfloat16, device=dev)
     slices = zhi is not None and len(zhi) == _lib.SLICES
     entry = L.atf_decode_paged_slices_bf16 if slices else L.atf_decode_paged_bf16
     table = _lib.zhi_array(zhi, _lib.SLICES if slices else _lib.LEVELS)
+    if not seq_lens.is_contiguous():
+        seq_lens = seq_lens.contiguous()
     _lib.check(entry(
-        _lib.ptr(out), out.stride(0), out.stride(1), _lib.ptr(q), q.stride(0), q.stride(1),
-        _lib.ptr(k_cache), _lib.ptr(v_cache), k_cache.shape[0], _lib.ptr(page_table), page_table.shape[1],
-        _lib.ptr(seq_lens.contiguous()), B, Hq, hkv, int(max_seq_len), table, float(sm_scale),
-        _lib.ptr(rope_cs), max_pos, _layout(layout), _lib.ptr(ws), ws.numel() * 4, stream))
+        out.data_ptr(), Hq * _lib.HEAD_DIM, _lib.HEAD_DIM, q.data_ptr(), q_sb, q_sh,
+        k_cache.data_ptr(), v_cache.data_ptr(), num_pages, page_table.data_ptr(), page_table.shape[1],
+        seq_lens.data_ptr(), B, Hq, hkv, int(max_seq_len), table, float(sm_scale),
+        _lib.ptr(rope_cs), max_pos, _layout(layout), ws[0], ws[1], stream))
     return out
 
 
