@@ -745,6 +745,109 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
   }
 }
 
+// ---- measurement probe: the MFMA ceiling of this kernel's structure ----
+// A pseudo-random bf16 value in about [-2, 2] (or [0, 1] for P), from a hash,
+// so that the matrix core switches as much as on real data (the part's power
+// limit, and with it the clock, depends on operand activity).
+__device__ __forceinline__ uint32_t probe_hash(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x7feb352dU;
+  x ^= x >> 15;
+  x *= 0x846ca68bU;
+  x ^= x >> 16;
+  return x;
+}
+__device__ __forceinline__ uint32_t probe_bf16x2(uint32_t h, bool unit) {
+  // sign (unless unit), exponent 126..128 (126..126 for unit), random mantissa, per half
+  uint32_t r = 0;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const uint32_t b = h >> (16 * k);
+    const uint32_t sign = unit ? 0u : (b & 1u);
+    const uint32_t ex = unit ? 126u : 126u + ((b >> 1) % 3u);
+    const uint32_t mant = (b >> 4) & 0x7fu;
+    r |= ((sign << 15) | (ex << 7) | mant) << (16 * k);
+  }
+  return r;
+}
+__device__ __forceinline__ u32x4 probe_vec(uint32_t seed, bool unit) {
+  return u32x4{probe_bf16x2(probe_hash(seed * 4 + 0), unit), probe_bf16x2(probe_hash(seed * 4 + 1), unit),
+               probe_bf16x2(probe_hash(seed * 4 + 2), unit), probe_bf16x2(probe_hash(seed * 4 + 3), unit)};
+}
+
+// The prefill kernel's MFMA work with nothing else: the same grid, block
+// mapping, waves, tile-pair count per workgroup (causal, nk = nq, window OFF),
+// LDS operand ring and stream order (PV of 8 pages then QK of 8 levels over
+// four 32-key blocks, 64 MFMAs per pair), s_setprio and the two barriers per
+// pair with the two wave groups one phase apart -- but no softmax, no K/V
+// copies (LDS holds random bf16 written once) and no masks.  Its time against
+// prefill_kernel's at the same shape is the cost of the softmax side and the
+// staging; its rate against the 2.5 PFLOP/s peak is the ceiling of the
+// structure at the clock the part's power limit allows.  The accumulators are
+// kept live by an empty asm statement and one store per lane at the end.
+__global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_mfma_probe_kernel(int nq, int hq, int n_qtiles,
+                                                                               float* sink) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
+  lds_u8* smem = (lds_u8*)(smem_raw);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int bid = blockIdx.x;
+  const int xcd = bid & 7;
+  const int j = bid >> 3;
+  const int h = j % hq;
+  const int qrank = (j / hq) * 8 + xcd;
+  const int qt = n_qtiles - 1 - qrank;
+  if (qt < 0) return;
+  const int last_wg = min(nq, qt * kPfRowsWg + kPfRowsWg) - 1;
+  const int T = min((nq + kPfTileN - 1) / kPfTileN, last_wg / kPfTileN + 1);
+  const int U = ((T + 1) & ~1) >> 1;
+  // random operands: LDS once, Q and P in registers
+  for (int i = tid; i < kPfLdsTotal / 16; i += kPfWaves * 64)
+    *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(smem + i * 16) =
+        probe_vec(static_cast<uint32_t>(i) * 977u + static_cast<uint32_t>(h), false);
+  u32x4 Qf[kLevels];
+  bf16x8 Pf[8];
+#pragma unroll
+  for (int l = 0; l < kLevels; ++l) Qf[l] = probe_vec(static_cast<uint32_t>((bid * 512 + tid) * 16 + l), false);
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    Pf[i] = __builtin_bit_cast(bf16x8, probe_vec(static_cast<uint32_t>((bid * 512 + tid) * 16 + 8 + i), true));
+  __syncthreads();
+  f32x16 O[4], S[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    O[i] = f32x16{};
+    S[i] = f32x16{};
+  }
+  const f32x16 C = f32x16{};
+  const int grp = wave >> 2;
+  const int k_lane = ((lane & 31) >> 4) * 4096 + (lane >> 5) * 256 + (lane & 15) * 16;
+  const int v_lane = (lane >> 5) * 512 + (lane & 31) * 16;
+  if (grp == 1) pf_barrier();  // group 1 starts one step late
+  for (int u = 0; u <= U; ++u) {
+    __builtin_amdgcn_s_setprio(1);
+    {
+      const lds_u8* kb = smem + (u % kPfKPairs) * kPfPairBytes + k_lane;
+      const lds_u8* vb = smem + kPfVRegion + ((u + 1) & 1) * kPfPairBytes + v_lane;
+      bf16x8 f[kRing];
+      pv_prefetch(vb, f);
+      pv_stream(vb, kb, Pf, O, f);
+      qk_stream<kLevels>(kb, f, Qf, C, S);
+    }
+    __builtin_amdgcn_s_setprio(0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) asm volatile("" ::"v"(S[i]));  // the QK results stay live
+    pf_barrier();
+    pf_barrier();  // the other group's MFMA phase
+  }
+  if (grp == 0) pf_barrier();  // group 0 ends one step late
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc += O[i][0] + S[i][0];
+  sink[static_cast<int64_t>(bid) * (kPfWaves * 64) + tid] = acc;
+}
+
 // Level count per (32-row tile, 32-key block) through the LevelWalker the
 // attention kernel uses (even blocks are the far half of a 64-key tile, odd
 // blocks the near half); out is [n_row_tiles][n_kblocks].
@@ -764,8 +867,9 @@ constexpr int kPfMaxDevices = 64;
 std::mutex g_attr_mu;
 bool g_attr_set[kPfMaxDevices];  // the 160 KB dynamic-LDS attribute is set on this device
 
-// Both prefill kernels may use all 160 KB of LDS: the attribute is set once per
-// device (the current one), under a lock, before the first launch there.
+// The prefill kernels (and the probe) may use all 160 KB of LDS: the attribute
+// is set once per device (the current one), under a lock, before the first
+// launch there.
 hipError_t ensure_lds_attribute() {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
@@ -774,7 +878,8 @@ hipError_t ensure_lds_attribute() {
   std::lock_guard<std::mutex> lock(g_attr_mu);
   if (g_attr_set[dev]) return hipSuccess;
   for (const void* f : {reinterpret_cast<const void*>(prefill_kernel<false>),
-                        reinterpret_cast<const void*>(prefill_kernel<true>)}) {
+                        reinterpret_cast<const void*>(prefill_kernel<true>),
+                        reinterpret_cast<const void*>(prefill_mfma_probe_kernel)}) {
     e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kPfLdsTotal);
     if (e != hipSuccess) return e;
   }
@@ -791,6 +896,16 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t s) {
     hipLaunchKernelGGL(prefill_kernel<false>, dim3(blocks), dim3(kPfWaves * 64), kPfLdsTotal, s, a);
   else
     hipLaunchKernelGGL(prefill_kernel<true>, dim3(blocks), dim3(kPfWaves * 64), kPfLdsTotal, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_prefill_mfma_probe(float* sink, int nq, int hq, hipStream_t s) {
+  if (nq <= 0 || hq <= 0) return hipSuccess;
+  if (hipError_t e = ensure_lds_attribute(); e != hipSuccess) return e;
+  const int n_qtiles = (nq + kPfRowsWg - 1) / kPfRowsWg;
+  const int blocks = ((n_qtiles + 7) / 8) * hq * 8;
+  hipLaunchKernelGGL(prefill_mfma_probe_kernel, dim3(blocks), dim3(kPfWaves * 64), kPfLdsTotal, s, nq, hq, n_qtiles,
+                     sink);
   return hipGetLastError();
 }
 

@@ -287,6 +287,24 @@ def bench_gpu(args):
               + (f" (gfx clock median {clk['median']:.0f} MHz)" if clk else ""), flush=True)
     del kc, vc, table
 
+    # ---- the MFMA ceiling of the prefill's structure (same grid and MFMA
+    # stream, no softmax, no K/V staging), at the same shape ----
+    if args.only in ("all", "prefill"):
+        from atflash import _lib
+        blocks = -(-(-(-N // 256)) // 8) * 8 * HQ
+        sink = torch.empty(blocks * 512, dtype=torch.float32, device=dev)
+        fp = lambda: _lib.check(_lib.lib().atf_prefill_mfma_probe(sink.data_ptr(), N, HQ,  # noqa: E731
+                                                                  _lib.stream_of(dev)))
+        for _ in range(max(1, args.warmup // 2)):
+            fp()
+        with ClockSampler() as cs:
+            res["probe"] = _stats(_events_time(fp, args.steps))
+        res["clocks"]["prefill_probe"] = cs.summary()
+        clk = res["clocks"]["prefill_probe"].get("gfxclk_mhz") or {}
+        print(f"[bench] prefill MFMA-ceiling probe: {res['probe']['median_ms']:.3f} ms"
+              + (f" (gfx clock median {clk['median']:.0f} MHz)" if clk else ""), flush=True)
+        del sink
+
     # ---- decode: paged cache, permuted pages, pools rotated past the MALL ----
     n_pages = -(-N // 16)
     copies = max(1, math.ceil((1 << 30) / (n_pages * HKV * 8192)))
@@ -571,6 +589,19 @@ def _clk(summary):
         return None
 
 
+def _probe_summary(res, flops_off):
+    """The MFMA-ceiling probe beside the window-OFF kernel: its time, its
+    fraction of peak, its clock, and the kernel's time over the probe's."""
+    if "probe" not in res:
+        return None
+    t = res["probe"]["mean_ms"]
+    return {"kernel": "atf::prefill_mfma_probe_kernel (prefill's grid and MFMA/LDS operand stream; no softmax, "
+                      "no K/V staging)",
+            "ms": t, "frac": flops_off / (t * 1e-3) / PEAK_BF16,
+            "gfxclk_mhz": _clk(res["clocks"].get("prefill_probe")),
+            "kernel_ms_over_probe_ms": res["prefill_attn"]["off"]["mean_ms"] / t}
+
+
 def _frac_at_clock(frac, summary):
     """A fraction of the 2.5 PFLOP/s peak restated against the peak at the
     clock the section actually ran at (peak scales with the clock)."""
@@ -768,6 +799,7 @@ def main():
                      "unit": "TFLOP/s", "frac": roof["off"]["frac"], "traffic": roof["off"]["traffic"],
                      "kernel": "atf::prefill_kernel, window OFF",
                      "gfxclk_mhz": _clk(res["clocks"].get("prefill_attn_off")),
+                     "ceiling_probe": _probe_summary(res, flops_off),
                      "frac_of_peak_at_measured_clock": _frac_at_clock(roof["off"]["frac"],
                                                                       res["clocks"].get("prefill_attn_off")),
                      "per_window": roof},

@@ -196,6 +196,18 @@ int atf_decode_paged_bf16_noalloc(void* out, int64_t o_sb, int64_t o_sh,
                                   int layout, void* stream);
 
 /*
+ * Measurement only; no counterpart in the reference.  Runs the prefill
+ * kernel's matrix-core work for a causal window-OFF prefill of nq tokens and
+ * num_q_heads q heads (one sequence) with nothing else: the same grid, waves,
+ * LDS operand ring, MFMA order, priorities and barriers, but no softmax, no
+ * K/V staging and random operands.  Its time beside atf_prefill_bf16's at the
+ * same shape measures the ceiling of the kernel's structure at the clock the
+ * part runs it at.  sink: device fp32 of ceil(ceil(nq / 256) / 8) * 8 *
+ * num_q_heads * 512 elements (overwritten).
+ */
+int atf_prefill_mfma_probe(float* sink, int nq, int num_q_heads, void* stream);
+
+/*
  * Per-tile level counts (D_eff / 16) as the kernels compute them, for tests of
  * the integer window path.  prefill: out int32 [n_row_tiles][n_kblocks] for
  * 32-row query tiles starting at q_offset + 32*i and 32-key blocks;
