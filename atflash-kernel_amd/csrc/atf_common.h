@@ -106,6 +106,26 @@ __device__ __forceinline__ u32x4 load_slice(const uint16_t* row, int layout, int
   return *reinterpret_cast<const u32x4*>(row + 8 * s);
 }
 
+// Slices s0 + stride * i (i = 0..3) of an input row, as load_slice reads them,
+// with the layout test outside the loads so that all of them are issued before
+// any is waited for.
+template <int kStride>
+__device__ __forceinline__ void load_slices4(const uint16_t* row, int layout, int s0, u32x4 (&out)[4]) {
+  if (layout == kLayoutHalfSplit) {
+    u32x2 x1[4], x2[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x1[i] = *reinterpret_cast<const u32x2*>(row + slice_pair0(s0 + kStride * i));
+      x2[i] = *reinterpret_cast<const u32x2*>(row + kP + slice_pair0(s0 + kStride * i));
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = u32x4{x1[i][0], x1[i][1], x2[i][0], x2[i][1]};
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = *reinterpret_cast<const u32x4*>(row + 8 * (s0 + kStride * i));
+  }
+}
+
 // Slot of token t (0..15) inside a transposed V page: token groups of 4 are
 // stored in the order {0, 2, 1, 3}.
 __device__ __forceinline__ int v_slot(int t) {

@@ -228,25 +228,26 @@ void decode_kernel(const int32_t* page_table, const int32_t* seq_lens, const uin
   for (int u = 0; u < kDecUnroll; ++u) ent[u] = dec_fetch_entry(row, p_first + kStride + u, p_begin, p_end);
 
   // ---- Q^T fragments: lane holds q head g, slice 4 lp + lane/16 ----
+  // Every Q and (cos, sin) load is issued before any is used (one memory round
+  // trip, not one per slice): lanes past the group read the group's last head
+  // and a sequence of length 0 reads position 0, both in bounds, and are
+  // zeroed afterwards.
   u32x4 Qf[4];
   {
-    const int qh = h * a.group + g;
+    const int qh = h * a.group + min(g, a.group - 1);
     const bool valid = g < a.group && N > 0;
     const uint16_t* qrow = a.q + static_cast<int64_t>(b) * a.q_sb + static_cast<int64_t>(qh) * a.q_sh;
+    load_slices4<4>(qrow, a.layout, lane >> 4, Qf);
+    if (a.rope_cs != nullptr) {
+      float cs[4][8];
 #pragma unroll
-    for (int lp = 0; lp < 4; ++lp) {
-      u32x4 v = {0u, 0u, 0u, 0u};
-      const int sl = 4 * lp + (lane >> 4);
-      if (valid) {
-        v = load_slice(qrow, a.layout, sl);
-        if (a.rope_cs != nullptr) {
-          float cs[8];
-          load_cs4(a.rope_cs, N - 1, slice_pair0(sl), cs);
-          v = rope_slice(v, cs);
-        }
-      }
-      Qf[lp] = v;
+      for (int lp = 0; lp < 4; ++lp) load_cs4(a.rope_cs, max(N - 1, 0), slice_pair0(4 * lp + (lane >> 4)), cs[lp]);
+#pragma unroll
+      for (int lp = 0; lp < 4; ++lp) Qf[lp] = rope_slice(Qf[lp], cs[lp]);
     }
+#pragma unroll
+    for (int lp = 0; lp < 4; ++lp)
+      if (!valid) Qf[lp] = u32x4{0u, 0u, 0u, 0u};
   }
   // per-key rule: the distance limit of this lane's slice in each quad
   int zl[4] = {0, 0, 0, 0};

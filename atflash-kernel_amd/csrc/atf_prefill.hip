@@ -460,26 +460,31 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
 
   // ---- Q fragments (B operand of S^T = K Q^T), with RoPE and the log2-unit
   // softmax scale applied at load ----
+  // Every Q and (cos, sin) load is issued before any is used, four levels at a
+  // time (one memory round trip per four levels instead of one per level):
+  // rows past nq read row nq - 1, in bounds, and are zeroed afterwards.
   u32x4 Qf[kLevels];
   const bool second = lane >= 32;
   const int row = lr0 + (lane & 31);
   {
-    const uint16_t* qrow = a.q + static_cast<int64_t>(b) * a.q_sb + static_cast<int64_t>(row) * a.q_st +
+    const int row_c = min(row, a.nq - 1);
+    const uint16_t* qrow = a.q + static_cast<int64_t>(b) * a.q_sb + static_cast<int64_t>(row_c) * a.q_st +
                            static_cast<int64_t>(h) * a.q_sh;
+    // k half h of level l is slice 2l + h, as in the cache's K pages
 #pragma unroll
-    for (int l = 0; l < kLevels; ++l) {
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (row < a.nq) {
-        // k half h of level l is slice 2l + h, as in the cache's K pages
-        const int sl = 2 * l + (second ? 1 : 0);
-        v = load_slice(qrow, a.layout, sl);
-        if (a.rope_cs != nullptr) {
-          float cs[8];
-          load_cs4(a.rope_cs, a.q_offset + row, slice_pair0(sl), cs);
-          v = rope_slice(v, cs, a.scale_log2);
-        }
+    for (int j = 0; j < 2; ++j) {
+      u32x4 v[4];
+      const int s0 = 8 * j + (second ? 1 : 0);  // levels 4j .. 4j+3: slices s0, s0+2, s0+4, s0+6
+      load_slices4<2>(qrow, a.layout, s0, v);
+      if (a.rope_cs != nullptr) {
+        float cs[4][8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) load_cs4(a.rope_cs, a.q_offset + row_c, slice_pair0(s0 + 2 * i), cs[i]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = rope_slice(v[i], cs[i], a.scale_log2);
       }
-      Qf[l] = v;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) Qf[4 * j + i] = (row < a.nq) ? v[i] : u32x4{0u, 0u, 0u, 0u};
     }
   }
 
