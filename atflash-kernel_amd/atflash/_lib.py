@@ -57,6 +57,7 @@ SIGNATURES = {
     "atf_decode_paged_bf16_noalloc": (_i, [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i, _p, _i, _p,
                                            _i, _i, _i, _i, _p, _f, _p, _i, _i, _p]),
     "atf_prefill_mfma_probe": (_i, [_p, _i, _i, _p]),
+    "atf_decode_stream_probe": (_i, [_p, _sz, _p, _p, _i, _p, _i, _p, _i, _i, _i, _p]),
     "atf_prefill_tile_levels": (_i, [_p, _i, _i, _i, _p, _p]),
     "atf_decode_page_levels": (_i, [_p, _i, _i, _p, _p]),
 }

@@ -400,6 +400,35 @@ int atf_prefill_mfma_probe(float* sink, int nq, int num_q_heads, void* stream) {
   return ok();
 }
 
+int atf_decode_stream_probe(uint32_t* sink, size_t sink_bytes, const void* k_cache, const void* v_cache,
+                            int num_pages, const int32_t* page_table, int max_pages, const int32_t* seq_lens,
+                            int batch, int num_kv_heads, int max_seq_len, void* stream) {
+  if (!sink || !k_cache || !v_cache || !page_table || !seq_lens) return fail(ATF_ERR_INVALID, "null pointer argument");
+  if (batch <= 0 || num_kv_heads <= 0 || max_seq_len <= 0 || max_seq_len >= (1 << 24) || num_pages <= 0 ||
+      max_pages <= 0 || static_cast<int64_t>(max_pages) * atf::kPage < max_seq_len)
+    return fail(ATF_ERR_INVALID, "bad arguments");
+  if (!aligned(k_cache, 16) || !aligned(v_cache, 16)) return fail(ATF_ERR_INVALID, "caches must be 16-byte aligned");
+  atf::DecodeArgs a{};
+  int ns = 1, pps = 1, waves = 0;
+  decode_split(batch, num_kv_heads, max_seq_len, &ns, &pps, &waves);
+  const size_t need = static_cast<size_t>(batch) * num_kv_heads * ns * atf::kDecWaves * sizeof(uint32_t);
+  if (sink_bytes < need) return fail(ATF_ERR_WORKSPACE, "probe sink of %zu bytes required, got %zu", need, sink_bytes);
+  a.k_cache = static_cast<const uint16_t*>(k_cache);
+  a.v_cache = static_cast<const uint16_t*>(v_cache);
+  a.num_pages = num_pages;
+  a.page_table = page_table;
+  a.max_pages = max_pages;
+  a.seq_lens = seq_lens;
+  a.max_seq_len = max_seq_len;
+  a.batch = batch;
+  a.hkv = num_kv_heads;
+  a.n_splits = ns;
+  a.pages_per_split = pps;
+  hipError_t e = atf::launch_decode_stream_probe(a, sink, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "probe launch");
+  return ok();
+}
+
 int atf_prefill_tile_levels(int32_t* out, int n_row_tiles, int n_kblocks, int q_offset, const int32_t* zhi,
                             void* stream) {
   if (!out || n_row_tiles < 0 || n_kblocks < 0 || q_offset < 0) return fail(ATF_ERR_INVALID, "bad arguments");

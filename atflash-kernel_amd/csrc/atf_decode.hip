@@ -388,6 +388,59 @@ void decode_kernel(const int32_t* page_table, const int32_t* seq_lens, const uin
   }
 }
 
+// ---- measurement probe: the streaming ceiling of the decode's page loads ----
+// decode_kernel's grid, waves, split rule (window OFF), page-table fetches and
+// page loads (the same range-checked, non-temporal buffer loads, the same
+// 4-page groups with the rolling reload), with the compute replaced by an
+// XOR of the loaded words, no LDS combine and no merge: what the memory
+// system delivers to this access pattern.  One word per wave goes to
+// sink[((b * hkv + h) * n_splits + s) * kDecWaves + wave].
+__global__ __launch_bounds__(kDecWaves * 64) __attribute__((amdgpu_waves_per_eu(2)))
+void decode_stream_probe_kernel(const int32_t* page_table, const int32_t* seq_lens, const uint16_t* k_cache,
+                                const uint16_t* v_cache, int max_pages, int pages_per_split, int max_seq_len,
+                                int hkv, int num_pages, int n_splits, uint32_t* sink) {
+  const DecHot hot{page_table, seq_lens, k_cache, v_cache, max_pages, pages_per_split, max_seq_len, hkv, num_pages};
+  const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int p_begin = s * hot.pages_per_split;
+  constexpr int kStride = kDecUnroll * kDecWaves;
+  const int p_first = p_begin + kDecUnroll * __builtin_amdgcn_readfirstlane(wave);
+  int ent[kDecUnroll];
+  const int32_t* row = hot.page_table + static_cast<int64_t>(b) * hot.max_pages;
+#pragma unroll
+  for (int u = 0; u < kDecUnroll; ++u) ent[u] = row[min(p_first + u, hot.max_pages - 1)];
+  const int N = max(0, min(hot.seq_lens[b], hot.max_seq_len));
+  const int n_pages = (N + kPage - 1) / kPage;
+  const int p_end = min(n_pages, p_begin + hot.pages_per_split);
+  PageRegs pr[kDecUnroll];
+#pragma unroll
+  for (int u = 0; u < kDecUnroll; ++u)
+    dec_load_page(hot, h, ent[u], p_first + u < p_end, p_first + u, kSlices, false, lane, pr[u]);
+#pragma unroll
+  for (int u = 0; u < kDecUnroll; ++u) ent[u] = dec_fetch_entry(row, p_first + kStride + u, p_begin, p_end);
+  uint32_t acc = 0;
+  for (int p0 = p_first; p0 < p_end; p0 += kStride) {
+#pragma unroll
+    for (int u = 0; u < kDecUnroll; ++u) {
+      if (p0 + u >= p_end) break;
+      PageRegs& r = pr[u];
+#pragma unroll
+      for (int lp = 0; lp < 4; ++lp) acc ^= r.k[lp][0] ^ r.k[lp][1] ^ r.k[lp][2] ^ r.k[lp][3];
+#pragma unroll
+      for (int db = 0; db < 8; ++db) acc ^= r.v[db][0] ^ r.v[db][1];
+      const int pn = p0 + kStride + u;
+      if (pn < p_end) {
+        dec_load_page(hot, h, ent[u], true, pn, kSlices, false, lane, pr[u]);
+        ent[u] = dec_fetch_entry(row, pn + kStride, p_begin, p_end);
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) acc ^= static_cast<uint32_t>(__shfl_xor(static_cast<int>(acc), m));
+  if (lane == 0) sink[((static_cast<int64_t>(b) * hkv + h) * n_splits + s) * kDecWaves + wave] = acc;
+}
+
 // Log-sum-exp merge of the split partials, launched after decode_kernel when
 // n_splits > 1.  One workgroup per (dim chunk of 32, kv head, sequence), so
 // that the merge's loads spread over 4 CUs per (sequence, kv head): a single
@@ -575,6 +628,14 @@ hipError_t launch_decode_noalloc(DecodeArgs a, hipStream_t s) {
   a.ws_ml = reinterpret_cast<float*>(base);
   a.ws_o = a.ws_ml + static_cast<size_t>(a.batch) * a.hkv * a.n_splits * kDecMaxGroup * 2;
   return launch_decode(a, s);
+}
+
+hipError_t launch_decode_stream_probe(const DecodeArgs& a, uint32_t* sink, hipStream_t s) {
+  if (a.batch <= 0) return hipSuccess;
+  hipLaunchKernelGGL(decode_stream_probe_kernel, dim3(a.n_splits, a.hkv, a.batch), dim3(kDecWaves * 64), 0, s,
+                     a.page_table, a.seq_lens, a.k_cache, a.v_cache, a.max_pages, a.pages_per_split, a.max_seq_len,
+                     a.hkv, a.num_pages, a.n_splits, sink);
+  return hipGetLastError();
 }
 
 hipError_t launch_decode_page_levels(int32_t* out, int n_pages, int seq_len, const LevelTable& lt,

@@ -100,6 +100,9 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t s);
 // launch_decode with the workspace pointers taken from the device's fixed
 // scratch (a.ws_ml and a.ws_o are set here).
 hipError_t launch_decode_noalloc(DecodeArgs a, hipStream_t s);
+// The streaming probe of the decode (measurement only): 8-wave workgroups
+// over a.n_splits x a.hkv x a.batch; sink holds one word per wave.
+hipError_t launch_decode_stream_probe(const DecodeArgs& a, uint32_t* sink, hipStream_t s);
 hipError_t launch_decode_page_levels(int32_t* out, int n_pages, int seq_len, const LevelTable& lt,
                                      hipStream_t s);
 

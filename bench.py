@@ -356,6 +356,24 @@ def bench_gpu(args):
         res["decode"][name]["graph_mean_ms"] = _graph_time(fn, 8 * copies)
         print(f"[bench] decode {name}: {res['decode'][name]['batch_mean_ms'] * 1e3:.2f} us per call "
               f"(graph replay {res['decode'][name]['graph_mean_ms'] * 1e3:.2f} us)", flush=True)
+    # ---- the streaming ceiling of the decode's page loads (same grid and
+    # loads, no compute, no merge), over the same rotated pools ----
+    if args.only in ("all", "decode"):
+        from atflash import _lib
+        sink = torch.empty(HKV * 256 * 8, dtype=torch.int32, device=dev)
+        it = [0]
+
+        def fp():
+            i = it[0] % copies
+            it[0] += 1
+            _lib.check(_lib.lib().atf_decode_stream_probe(
+                sink.data_ptr(), sink.numel() * 4, caches[i].k.data_ptr(), caches[i].v.data_ptr(), n_pages,
+                tables[i].data_ptr(), n_pages, seq.data_ptr(), 1, HKV, N, _lib.stream_of(dev)))
+        for _ in range(args.warmup * 10):
+            fp()
+        res["decode_probe"] = {"batch_mean_ms": _events_time_batch(fp, args.steps * 40)}
+        print(f"[bench] decode streaming probe: {res['decode_probe']['batch_mean_ms'] * 1e3:.2f} us per call",
+              flush=True)
     res["decode_pool_bytes"] = copies * n_pages * HKV * 8192
     return res
 
@@ -602,6 +620,18 @@ def _probe_summary(res, flops_off):
             "kernel_ms_over_probe_ms": res["prefill_attn"]["off"]["mean_ms"] / t}
 
 
+def _decode_probe_summary(res, N):
+    """The decode's streaming probe beside the window-OFF call: its time per
+    call, its rate against 8 TB/s, and the call's time over the probe's."""
+    if "decode_probe" not in res or "off" not in res["decode"]:
+        return None
+    t = res["decode_probe"]["batch_mean_ms"] * 1e-3
+    nbytes = N * HKV * D * 2 * 2
+    return {"kernel": "atf::decode_stream_probe_kernel (the decode's grid and page loads; no compute, no merge)",
+            "us_per_launch": t * 1e6, "GBps": nbytes / t / 1e9, "frac": nbytes / t / PEAK_HBM,
+            "call_us_over_probe_us": res["decode"]["off"]["batch_mean_ms"] * 1e-3 / t}
+
+
 def _frac_at_clock(frac, summary):
     """A fraction of the 2.5 PFLOP/s peak restated against the peak at the
     clock the section actually ran at (peak scales with the clock)."""
@@ -805,7 +835,8 @@ def main():
                      "per_window": roof},
         "roofline_decode": {"bound": "hbm", "achieved": dec["off"]["GBps"], "peak": PEAK_HBM / 1e9,
                             "unit": "GB/s", "frac": dec["off"]["frac"], "traffic": dec["off"]["traffic"],
-                            "kernel": "atf::decode_kernel, window OFF", "per_window": dec},
+                            "kernel": "atf::decode_kernel, window OFF", "per_window": dec,
+                            "ceiling_probe": _decode_probe_summary(res, N)},
         "roofline_kv_write": {"bound": "hbm", "achieved": kvw["GBps"], "peak": PEAK_HBM / 1e9, "unit": "GB/s",
                               "frac": kvw["frac"], "traffic": kvw["traffic"], "bytes": kvw_bytes,
                               "kernel": f"atf::kv_write_kernel, {N} tokens x {HKV} kv heads",

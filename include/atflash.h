@@ -208,6 +208,22 @@ int atf_decode_paged_bf16_noalloc(void* out, int64_t o_sb, int64_t o_sh,
 int atf_prefill_mfma_probe(float* sink, int nq, int num_q_heads, void* stream);
 
 /*
+ * Measurement only; no counterpart in the reference.  Streams the pages a
+ * window-OFF decode of this shape reads (the same split grid as
+ * atf_decode_paged_bf16, always as 8-wave workgroups -- the decode's own
+ * shape wherever its splits hold 32 pages or more, as at 128K -- the same
+ * page-table fetches and range-checked non-temporal page loads in 4-page
+ * groups) with the compute
+ * replaced by an XOR of the loaded words, and no merge: the rate the memory
+ * system gives this access pattern, for comparison with the decode call.
+ * sink: device uint32, at least batch x num_kv_heads x n_splits x 8 words
+ * (n_splits <= 256); ATF_ERR_WORKSPACE if sink_bytes is smaller.
+ */
+int atf_decode_stream_probe(uint32_t* sink, size_t sink_bytes, const void* k_cache, const void* v_cache,
+                            int num_pages, const int32_t* page_table, int max_pages, const int32_t* seq_lens,
+                            int batch, int num_kv_heads, int max_seq_len, void* stream);
+
+/*
  * Per-tile level counts (D_eff / 16) as the kernels compute them, for tests of
  * the integer window path.  prefill: out int32 [n_row_tiles][n_kblocks] for
  * 32-row query tiles starting at q_offset + 32*i and 32-key blocks;
