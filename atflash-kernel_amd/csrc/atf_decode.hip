@@ -81,45 +81,28 @@ struct DecHot {
   int max_pages, pages_per_split, max_seq_len, hkv, num_pages;
 };
 
-// Slice count of a key at a fixed offset in its page as the page index p walks
-// up (per-slice table, per-key rule): slice s is read from page
-// P_s = ceil((anchor - zhi8[s]) / 16) on, anchor = N-1 - offset, so
-// n(p) = #{s : P_s <= p}.  advance(p) costs one compare per page except when a
-// slice boundary is crossed (at most 16 times), laid out as the unlikely path.
-struct SliceWalker {
-  int n;
-  int next;
-  int anchor;
-  __device__ __forceinline__ int start_page(const SliceTable& st, int s) const {
-    const int z = min(st.zhi[s], 1 << 30);
-    return (anchor - z + kPage - 1) >> 4;  // ceil((anchor - zhi) / 16), arithmetic shift
-  }
-  __device__ __forceinline__ void init(const SliceTable& st, int anchor_) {
-    anchor = anchor_;
-    n = 0;
-    next = start_page(st, 0);
-  }
-  __device__ __forceinline__ int advance(const SliceTable& st, int p) {
-    while (__builtin_expect(p >= next, 0)) {
-      ++n;
-      next = (n < kSlices) ? start_page(st, n) : 0x7fffffff;
-    }
-    return n;
-  }
-};
-
 // The slices page p reads and whether an older key of it reads fewer.  Page
 // rule (level table): 2 L(p) slices, L(p) = levels of the youngest key's age.
-// Per-key rule: the youngest key's slices; a slice boundary falls inside the
-// page when the oldest key's count differs.
+// Per-key rule: the youngest key's slices, #{s : zhi8[s] >= age}; a slice
+// boundary falls inside the page when the oldest key's count differs.  Both
+// counts are straight-line scalar compares over the table (kernel-argument
+// SGPRs): 0.4 us per call faster at 128K than walking the slice boundaries
+// page by page with a loop, whose branches sat in front of every page load.
 template <bool kPerKey>
-__device__ __forceinline__ void page_slices(const DecodeArgs& a, SliceWalker& young, SliceWalker& old, int p, int N,
-                                            int& ns, bool& mask) {
+__device__ __forceinline__ void page_slices(const DecodeArgs& a, int p, int N, int& ns, bool& mask) {
+  const int z_young = (N - 1) - (p * kPage + kPage - 1);
   if constexpr (kPerKey) {
-    ns = young.advance(a.st, p);
-    mask = old.advance(a.st, p) != ns;
+    const int z_old = z_young + kPage - 1;
+    int cy = 0, co = 0;
+#pragma unroll
+    for (int s = 0; s < kSlices; ++s) {
+      cy += (a.st.zhi[s] >= z_young) ? 1 : 0;
+      co += (a.st.zhi[s] >= z_old) ? 1 : 0;
+    }
+    ns = cy;
+    mask = co != cy;
   } else {
-    ns = 2 * levels_of(a.lt, max(0, (N - 1) - (p * kPage + kPage - 1)));
+    ns = 2 * levels_of(a.lt, max(0, z_young));
     mask = false;
   }
 }
@@ -206,22 +189,14 @@ void decode_kernel(const int32_t* page_table, const int32_t* seq_lens, const uin
   // path, so that each page is waited for with the later pages' loads still in
   // flight, measured slower.)
   PageRegs pr[kDecUnroll];
-  // per-key rule: slice walkers for the youngest (offset 15) and oldest key of a page
-  SliceWalker wy, wo;
-  if constexpr (kPerKey) {
-    wy.init(a.st, (N - 1) - (kPage - 1));
-    wo.init(a.st, N - 1);
-  }
-  // Straight-line code up to the first page loads of the level rule (a page
-  // past the split gets an empty buffer range: its loads return zeros without
-  // a memory request), so the compiler reads every kernel argument they need in
-  // the first batch.  (The per-key rule's walkers branch; counting its first
-  // group's slices branch-free instead cost more than it saved.)
+  // Straight-line code up to the first page loads (a page past the split gets
+  // an empty buffer range: its loads return zeros without a memory request), so
+  // the compiler reads every kernel argument they need in the first batch.
 #pragma unroll
   for (int u = 0; u < kDecUnroll; ++u) {
     int ns;
     bool mask;
-    page_slices<kPerKey>(a, wy, wo, p_first + u, N, ns, mask);
+    page_slices<kPerKey>(a, p_first + u, N, ns, mask);
     dec_load_page(hot, h, ent[u], p_first + u < p_end, p_first + u, ns, mask, lane, pr[u]);
   }
 #pragma unroll
@@ -335,7 +310,7 @@ void decode_kernel(const int32_t* page_table, const int32_t* seq_lens, const uin
       if (pn < p_end) {
         int ns;
         bool mask;
-        page_slices<kPerKey>(a, wy, wo, pn, N, ns, mask);
+        page_slices<kPerKey>(a, pn, N, ns, mask);
         dec_load_page(hot, h, ent[u], true, pn, ns, mask, lane, pr[u]);
         ent[u] = dec_fetch_entry(row, pn + kStride, p_begin, p_end);
       }
