@@ -24,7 +24,7 @@
 // Merging: the 8 wave partials (m, l, o) of a split are combined in LDS.  With
 // one split per (sequence, kv head) the workgroup writes the output itself.
 // Otherwise it stores the split's partial in the workspace and ends, and a
-// second kernel (decode_merge_kernel, four workgroups per (sequence, kv head))
+// second kernel (decode_merge_kernel, eight workgroups per (sequence, kv head))
 // merges the split partials by log-sum-exp and writes the output.  The kernel
 // boundary orders the partial stores before the merge loads, so no workgroup
 // waits on another inside a launch: no arrival counters, atomics or fences.
@@ -439,19 +439,25 @@ void decode_stream_probe_kernel(const int32_t* page_table, const int32_t* seq_le
 }
 
 // Log-sum-exp merge of the split partials, launched after decode_kernel when
-// n_splits > 1.  One workgroup per (dim chunk of 32, kv head, sequence), so
-// that the merge's loads spread over 4 CUs per (sequence, kv head): a single
+// n_splits > 1.  One workgroup per (dim chunk, kv head, sequence), so that the
+// merge's loads spread over kMergeChunks CUs per (sequence, kv head): a single
 // workgroup per (sequence, kv head) issued 4x as many loads from one CU and
-// took about as long as the tail it replaced.  Thread t takes dims
-// 32 * chunk + 4 * (t % 8) .. +3 of query head mg and every H-th split
-// starting at hh (H = 8 split groups for G <= 8, 4 for larger groups).  It
-// loads the (m, l) and o of up to kBatch splits before using any of them, so
-// with up to 32 splits per thread the merge costs one memory round trip; more
-// splits are folded in batch by batch with a running max.  The H partial
-// merges of a (head, dims) sit in lanes of one wave and are combined by
-// cross-lane exchanges, without LDS or a workgroup barrier.
-constexpr int kMergeChunks = 4;
-constexpr int kMergeDims = kD / kMergeChunks;  // 32
+// took about as long as the tail it replaced.  Thread t takes 4 dims of its
+// chunk and, for query head mg, every H-th split starting at hh (H = the rows
+// of a wave for G <= 8, half of them for larger groups).  It loads the (m, l)
+// and o of up to kMergeBatch splits before using any of them, so with up to
+// 256 splits (G <= 8) the merge costs one memory round trip; more splits are
+// folded in batch by batch with a running max.  The H partial merges of a
+// (head, dims) sit in lanes of one wave and are combined by cross-lane
+// exchanges, without LDS or a workgroup barrier.
+constexpr int kMergeChunks = 8;
+constexpr int kMergeDims = kD / kMergeChunks;          // dims per workgroup
+constexpr int kMergeLanes = kMergeDims / 4;            // lanes per (head, split group), 4 dims each
+constexpr int kMergeRowsPerWave = 64 / kMergeLanes;    // (head, split group) rows per wave
+constexpr int kMergeBatch = 256 / kMergeRowsPerWave;   // splits loaded per thread before use
+static_assert(kMergeChunks * kMergeDims == kD && (kMergeLanes & (kMergeLanes - 1)) == 0 && kMergeLanes <= 32 &&
+                  kDecMaxGroup <= 16,
+              "merge layout: one or two heads per wave (8 waves: 8 heads for G <= 8, 16 for larger groups)");
 
 // The merge kernel's arguments are scalars (14 dwords), preloaded into SGPRs
 // with the dispatch, so the partial loads are issued at once instead of after
@@ -491,24 +497,20 @@ __global__ __launch_bounds__(512) void decode_merge_kernel(const float* ws_ml, c
   const float NEG_INF = -__builtin_huge_valf();
   const float c = a.scale_log2;
   const int64_t pbase = (static_cast<int64_t>(b) * a.hkv + h) * a.n_splits * kDecMaxGroup;  // split 0, head 0
-  constexpr int kBatch = 32;
-  // H split groups per (head, dims), 8 threads per group (4 dims each): the H
-  // groups of a head are lanes 8 hh + (t % 8) of one wave (H = 8 for G <= 8,
-  // 4 for larger groups), so their partial merges combine across lanes.
-  const int H = (a.group <= 8) ? 8 : 4;
-  const int row = tid >> 3;  // 0..63: (head, split group)
+  const int H = (a.group <= 8) ? kMergeRowsPerWave : kMergeRowsPerWave / 2;
+  const int row = tid / kMergeLanes;  // (head, split group)
   const int mg = row / H, hh = row - (row / H) * H;
-  const int q4 = 4 * (tid & 7);
+  const int q4 = 4 * (tid % kMergeLanes);
   const int md4 = chunk * kMergeDims + q4;
   const bool mact = mg < a.group;
   float m_t = NEG_INF, L_t = 0.f;
   f32x4 acc_t = f32x4{};
   if (mact) {
-    for (int j0 = hh; j0 < a.n_splits; j0 += kBatch * H) {
-      f32x2 mlv[kBatch];
-      f32x4 ov[kBatch];
+    for (int j0 = hh; j0 < a.n_splits; j0 += kMergeBatch * H) {
+      f32x2 mlv[kMergeBatch];
+      f32x4 ov[kMergeBatch];
 #pragma unroll
-      for (int j = 0; j < kBatch; ++j) {
+      for (int j = 0; j < kMergeBatch; ++j) {
         const int sp = j0 + j * H;
         mlv[j] = f32x2{NEG_INF, 0.f};
         ov[j] = f32x4{};
@@ -520,13 +522,13 @@ __global__ __launch_bounds__(512) void decode_merge_kernel(const float* ws_ml, c
       }
       float mb = m_t;
 #pragma unroll
-      for (int j = 0; j < kBatch; ++j) mb = fmaxf(mb, mlv[j][0]);
+      for (int j = 0; j < kMergeBatch; ++j) mb = fmaxf(mb, mlv[j][0]);
       if (mb != NEG_INF) {
         const float r = fast_exp2((m_t - mb) * c);  // m_t = -inf -> 0
         L_t *= r;
         acc_t *= r;
 #pragma unroll
-        for (int j = 0; j < kBatch; ++j) {
+        for (int j = 0; j < kMergeBatch; ++j) {
           const float wt = fast_exp2((mlv[j][0] - mb) * c);  // empty split: m = -inf -> 0
           L_t += wt * mlv[j][1];
           acc_t += wt * ov[j];
@@ -536,10 +538,9 @@ __global__ __launch_bounds__(512) void decode_merge_kernel(const float* ws_ml, c
     }
   }
   // every lane of the wave takes part in the exchanges (inactive rows hold an
-  // empty partial)
-  merge_xor(m_t, L_t, acc_t, 8, c);
-  merge_xor(m_t, L_t, acc_t, 16, c);
-  if (H == 8) merge_xor(m_t, L_t, acc_t, 32, c);
+  // empty partial); lanes kMergeLanes * k + (t % kMergeLanes), k < H, hold one
+  // (head, dims)
+  for (int mask = kMergeLanes; mask < kMergeLanes * H; mask *= 2) merge_xor(m_t, L_t, acc_t, mask, c);
   if (mact && hh == 0) {
     const float inv = L_t > 0.f ? 1.f / L_t : 0.f;
     uint16_t* out = a.out + static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(h * a.group + mg) * a.o_sh + md4;

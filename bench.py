@@ -211,6 +211,13 @@ def _events_time_batch(fn, n):
     return s.elapsed_time(e) / n
 
 
+def _events_time_median(fn, n, parts=5):
+    """Median over `parts` batches of n // parts back-to-back calls (ms per
+    call): where the host's launch work sets the pace (short contexts), one
+    batch carries whatever the host was doing meanwhile."""
+    return sorted(_events_time_batch(fn, max(1, n // parts)) for _ in range(parts))[parts // 2]
+
+
 def _graph_time(fn, calls, reps=5):
     """Average ms per call of `calls` calls captured in one HIP graph and
     replayed `reps` times under one event pair: the calls' GPU time without the
@@ -470,7 +477,7 @@ def bench_detail(steps=3):
                     return ops.decode_paged(q, pool.k, pool.v, t, seq, N, zhi, D ** -0.5, rt, 0)
                 for _ in range(10):
                     fn()
-                r[name + "_us"] = _events_time_batch(fn, 40 * steps) * 1e3
+                r[name + "_us"] = _events_time_median(fn, 40 * steps) * 1e3
                 r[name + "_graph_us"] = _graph_time(fn, 8 * copies) * 1e3
             r["on_over_off"] = r["off_us"] / r["k2_us"]
             r["on_over_off_graph"] = r["off_graph_us"] / r["k2_graph_us"]
