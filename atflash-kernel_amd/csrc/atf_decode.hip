@@ -439,25 +439,25 @@ void decode_stream_probe_kernel(const int32_t* page_table, const int32_t* seq_le
 }
 
 // Log-sum-exp merge of the split partials, launched after decode_kernel when
-// n_splits > 1.  One workgroup per (dim chunk, kv head, sequence), so that the
-// merge's loads spread over kMergeChunks CUs per (sequence, kv head): a single
-// workgroup per (sequence, kv head) issued 4x as many loads from one CU and
-// took about as long as the tail it replaced.  Thread t takes 4 dims of its
-// chunk and, for query head mg, every H-th split starting at hh (H = the rows
-// of a wave for G <= 8, half of them for larger groups).  It loads the (m, l)
-// and o of up to kMergeBatch splits before using any of them, so with up to
-// 256 splits (G <= 8) the merge costs one memory round trip; more splits are
-// folded in batch by batch with a running max.  The H partial merges of a
-// (head, dims) sit in lanes of one wave and are combined by cross-lane
-// exchanges, without LDS or a workgroup barrier.
+// n_splits > 1.  One workgroup per (16-dim chunk, kv head, sequence), so that
+// the merge's loads spread over 8 CUs per (sequence, kv head) (4 chunks of 32
+// dims were 0.6-0.75 us slower per call, 16 chunks of 8 dims 0.2 us).  Thread
+// t takes 4 dims of its chunk and, for query head mg, every H-th split
+// starting at hh (H = 16 for G <= 8, 8 for larger groups).  It loads the
+// (m, l) and o of up to kMergeBatch splits before using any of them, so with
+// up to 64 splits (32 for G > 8) the merge costs one memory round trip; more
+// splits are folded in batch by batch with a running max.  The H partial
+// merges of a (head, dims) sit in lanes 4k + (t % 4) of one wave (half wave
+// for G > 8) and are combined by DPP row rotations and permlane swaps, VALU
+// moves without LDS or a workgroup barrier.
 constexpr int kMergeChunks = 8;
 constexpr int kMergeDims = kD / kMergeChunks;          // dims per workgroup
 constexpr int kMergeLanes = kMergeDims / 4;            // lanes per (head, split group), 4 dims each
 constexpr int kMergeRowsPerWave = 64 / kMergeLanes;    // (head, split group) rows per wave
-constexpr int kMergeBatch = 256 / kMergeRowsPerWave;   // splits loaded per thread before use
-static_assert(kMergeChunks * kMergeDims == kD && (kMergeLanes & (kMergeLanes - 1)) == 0 && kMergeLanes <= 32 &&
-                  kDecMaxGroup <= 16,
-              "merge layout: one or two heads per wave (8 waves: 8 heads for G <= 8, 16 for larger groups)");
+constexpr int kMergeBatch = 4;                         // splits loaded per thread before use
+static_assert(kMergeChunks * kMergeDims == kD && kMergeLanes == 4 && kDecMaxGroup <= 16,
+              "merge layout: 4 lanes per (head, split group), one or two heads per wave (8 waves: 8 heads for "
+              "G <= 8, 16 for larger groups)");
 
 // The merge kernel's arguments are scalars (14 dwords), preloaded into SGPRs
 // with the dispatch, so the partial loads are issued at once instead of after
@@ -471,20 +471,80 @@ struct MergeArgs {
   float scale_log2;
 };
 
-// One (m, l, o) partial merged with the partial of lane ^ mask (a cross-lane
-// exchange within the wave, no LDS): both lanes end up holding the merge.
-__device__ __forceinline__ void merge_xor(float& m, float& l, f32x4& o, int mask, float c) {
+// Two (m, l, o) partials merged by log-sum-exp.
+__device__ __forceinline__ void merge_pair(float& m, float& l, f32x4& o, float mp, float lp, const f32x4& op,
+                                           float c) {
   const float NEG_INF = -__builtin_huge_valf();
-  const float mp = __shfl_xor(m, mask), lp = __shfl_xor(l, mask);
-  f32x4 op;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) op[i] = __shfl_xor(o[i], mask);
   const float M = fmaxf(m, mp);
   if (M != NEG_INF) {
     const float w = fast_exp2((m - M) * c), wp = fast_exp2((mp - M) * c);  // an empty side: m = -inf -> 0
     l = w * l + wp * lp;
     o = w * o + wp * op;
     m = M;
+  }
+}
+
+// Lane (l + n) % 16 of l's 16-lane row (DPP row rotation: a VALU move, no LDS).
+template <int kN>
+__device__ __forceinline__ float row_ror(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x120 + kN, 0xF, 0xF, false));
+}
+
+// The partial of lane l merged with those of lanes l + 4, l + 8, l + 12 of its
+// row (two row rotations), then with the rows l ^ 16 (and l ^ 32 when
+// `whole_wave`) by the gfx950 permlane swaps, which hand each lane the value of
+// the lane one row (two rows) away: afterwards every lane of a group {4h + q}
+// holds the merge of the group's partials.  Every lane takes part; the caller
+// keeps control flow uniform around it.
+__device__ __forceinline__ void merge_lane_groups(float& m, float& l, f32x4& o, bool whole_wave, float c) {
+  {
+    f32x4 op;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) op[i] = row_ror<8>(o[i]);
+    merge_pair(m, l, o, row_ror<8>(m), row_ror<8>(l), op, c);
+  }
+  {
+    f32x4 op;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) op[i] = row_ror<4>(o[i]);
+    merge_pair(m, l, o, row_ror<4>(m), row_ror<4>(l), op, c);
+  }
+  // a swap of a register with itself: result [0] holds rows (0, 0, 2, 2) and
+  // result [1] rows (1, 1, 3, 3) of the value (32-lane swap: halves (0, 0) and
+  // (1, 1)), so merging [0] with [1] merges each lane with its partner lane
+  auto swap16 = [](float x) {
+    return __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  };
+  auto swap32 = [](float x) {
+    return __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  };
+  {
+    const auto sm = swap16(m), sl = swap16(l);
+    f32x4 o0, o1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const auto so = swap16(o[i]);
+      o0[i] = __uint_as_float(so[0]);
+      o1[i] = __uint_as_float(so[1]);
+    }
+    m = __uint_as_float(sm[0]);
+    l = __uint_as_float(sl[0]);
+    o = o0;
+    merge_pair(m, l, o, __uint_as_float(sm[1]), __uint_as_float(sl[1]), o1, c);
+  }
+  if (whole_wave) {  // uniform over the launch
+    const auto sm = swap32(m), sl = swap32(l);
+    f32x4 o0, o1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const auto so = swap32(o[i]);
+      o0[i] = __uint_as_float(so[0]);
+      o1[i] = __uint_as_float(so[1]);
+    }
+    m = __uint_as_float(sm[0]);
+    l = __uint_as_float(sl[0]);
+    o = o0;
+    merge_pair(m, l, o, __uint_as_float(sm[1]), __uint_as_float(sl[1]), o1, c);
   }
 }
 
@@ -538,9 +598,9 @@ __global__ __launch_bounds__(512) void decode_merge_kernel(const float* ws_ml, c
     }
   }
   // every lane of the wave takes part in the exchanges (inactive rows hold an
-  // empty partial); lanes kMergeLanes * k + (t % kMergeLanes), k < H, hold one
-  // (head, dims)
-  for (int mask = kMergeLanes; mask < kMergeLanes * H; mask *= 2) merge_xor(m_t, L_t, acc_t, mask, c);
+  // empty partial); lanes 4k + (t % 4), k < H, hold one (head, dims): 16
+  // groups per wave for G <= 8, 8 per half wave above
+  merge_lane_groups(m_t, L_t, acc_t, H == 16, c);
   if (mact && hh == 0) {
     const float inv = L_t > 0.f ? 1.f / L_t : 0.f;
     uint16_t* out = a.out + static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(h * a.group + mg) * a.o_sh + md4;
