@@ -35,11 +35,12 @@ CASES = [
     ("qwen_g7_8192_k64", 8192, 28, 4, 1e7, 64.0, True),
     ("c1_g4_prerotated", 2048, 4, 1, 1e4, 2.0, False),
     ("narrow_window", 3000, 8, 2, 1e4, 0.3, True),
-    # GQA groups 1, 2 and 16: the split merge uses 8, 8 and 1 threads per (head, dims)
+    # GQA groups 1, 2 and 16: the split merge's two lane layouts (16 split groups
+    # per (head, dims) for G <= 8, 8 for larger groups)
     ("mha_g1", 5000, 4, 4, 1e4, 2.0, True),
     ("g2_off", 3000, 8, 4, 1e4, None, True),
     ("g16_k2", 6000, 16, 1, 5e5, 2.0, True),
-    # G = 16 with more splits than one merge batch (32) per thread
+    # G = 16 with 157 splits: five merge batches of 32 splits (4 per thread)
     ("g16_long_off", 40000, 16, 1, 5e5, None, True),
 ]
 
@@ -188,7 +189,8 @@ def test_workspace_reuse_with_more_sequences_and_heads(dev):
 
 
 def test_split_count_cap_long_sequence(dev):
-    """One kv head and 70000 tokens: the split count hits its cap (256 splits)."""
+    """One kv head and 70000 tokens: 244 splits (about the 256-workgroup target),
+    merged in four batches of 64 splits (4 per thread)."""
     g = torch.Generator().manual_seed(22)
     q = H.randn_bf16((8, H.D), g)
     k = H.randn_bf16((70000, 1, H.D), g)
