@@ -12,14 +12,15 @@ bf16 N(0,1) synthetic tensors from a fixed seed.
            N tokens whose pages are randomly permuted; four cache copies (> 1 GiB)
            are rotated so the 256 MB MALL cannot hold the working set;
   kv_write the paged-cache writer over the same N tokens (K rotated and
-           slice-blocked, V transposed into pages), timed as one batch of 4*K
-           back-to-back launches (`roofline_kv_write`, HBM bound).
+           slice-blocked, V transposed into pages), timed as back-to-back
+           launches, the median of five batches of 4*K/5 (`roofline_kv_write`,
+           HBM bound).
 A step is one such call.  W untimed warm-up steps, then exactly K timed steps per
 configuration (decode: 40*K), each bracketed by HIP events on the launch
 stream, with device synchronisation around the timed region.  Decode is also
-timed as one batch of 40*K back-to-back launches under a single event pair;
-that per-launch average (no event packets between launches) is the decode
-figure in `detail` and `roofline_decode`.
+timed as back-to-back launches under one event pair per batch of 8*K (the
+median of five batches); that per-launch average (no event packets between
+launches) is the decode figure in `detail` and `roofline_decode`.
 `value` is the window-ON (k = 2) prefill time in ms (lower is better); every
 configuration's numbers are in `detail`.
 roofline  prefill attention kernel (MFMA bound): algorithmic FLOPs per launch
@@ -332,7 +333,7 @@ def bench_gpu(args):
         for _ in range(args.warmup):
             fw()
         with ClockSampler() as cs:
-            res["kv_write"] = {"batch_mean_ms": _events_time_batch(fw, args.steps * 4)}
+            res["kv_write"] = {"batch_mean_ms": _events_time_median(fw, args.steps * 4)}
         res["clocks"]["kv_write"] = cs.summary()
         print(f"[bench] kv_write: {res['kv_write']['batch_mean_ms'] * 1e3:.1f} us", flush=True)
     qd = torch.randn((1, HQ, D), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
@@ -355,9 +356,10 @@ def bench_gpu(args):
             fn()
         with ClockSampler() as cs:
             res["decode"][name] = _stats(_events_time(fn, args.steps * 40))
-            # per-launch average over a batch with no event packets between launches:
-            # the figure the roofline uses (it matches the kernel trace's average)
-            res["decode"][name]["batch_mean_ms"] = _events_time_batch(fn, args.steps * 40)
+            # per-launch average over a batch with no event packets between launches
+            # (median over five batches): the figure the roofline uses (it matches
+            # the kernel trace's average)
+            res["decode"][name]["batch_mean_ms"] = _events_time_median(fn, args.steps * 40)
         res["clocks"]["decode_" + name] = cs.summary()
         # the same calls replayed from a HIP graph (no host launch work)
         res["decode"][name]["graph_mean_ms"] = _graph_time(fn, 8 * copies)
@@ -378,7 +380,7 @@ def bench_gpu(args):
                 tables[i].data_ptr(), n_pages, seq.data_ptr(), 1, HKV, N, _lib.stream_of(dev)))
         for _ in range(args.warmup * 10):
             fp()
-        res["decode_probe"] = {"batch_mean_ms": _events_time_batch(fp, args.steps * 40)}
+        res["decode_probe"] = {"batch_mean_ms": _events_time_median(fp, args.steps * 40)}
         print(f"[bench] decode streaming probe: {res['decode_probe']['batch_mean_ms'] * 1e3:.2f} us per call",
               flush=True)
     res["decode_pool_bytes"] = copies * n_pages * HKV * 8192
