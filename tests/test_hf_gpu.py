@@ -12,7 +12,14 @@ random-init Qwen2 model (2 layers, head_dim 128, GQA 4/2, RoPE base 1e4).
   through the whole model equals the single-shot one on the last logits and on
   layer 0's cached keys;
 * both RoPE modes of the hook: RoPE at load (the kernels rotate Q and K) and
-  HF's rotation (pre-rotated q and k).
+  HF's rotation (pre-rotated q and k);
+* a second model family with RoPE scaling: a random-init Llama with llama3
+  scaling (the Llama-3.1/3.2 form, base 5e5, 35 of the 64 frequency pairs
+  rescaled).  The hook rotates with the scaled inverse frequencies and takes
+  the window widths from the raw base, as the reference's integration does
+  (e2e_pipeline/atflash_e2e_fafi.py:138-172); the oracle model (HF's own
+  rotation, widths from the raw base) must agree for prefill, a decode step
+  and the paged cache.
 """
 import pytest
 import torch
@@ -38,21 +45,26 @@ def _model(dev):
     return m
 
 
-def _oracle_attention(module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kw):
-    """fp32 windowed attention on the CPU (the same tile rule as the kernels)."""
-    b, hq, L, d = query.shape
-    S = key.shape[-2]
-    qs, ks = OA.to_sorted(query.float().cpu()), OA.to_sorted(key.float().cpu())
-    vv = value.float().cpu()
-    w = WR.wavelengths_sorted(d, BASE, K_RET)
-    if L == 1:  # the hook decodes with the vec8 table, per-key rule (gates/g2_correctness.py:37-70)
-        z8 = WR.zhi_slice_vec8(d, BASE, K_RET)
-        hkv = ks.shape[1]
-        out = torch.stack([OA.ref_decode_sliced(qs[bi, :, 0], ks[bi].transpose(0, 1), vv[bi].transpose(0, 1), z8, 8)[0]
-                           for bi in range(b)])[:, :, None, :]
-    else:
-        out = OA.ref_window_attn(qs, ks, vv, w, phase="prefill", block_m=32, block_n=32, q_offset=S - L)
-    return out.transpose(1, 2).contiguous().to(query.dtype).to(query.device), None
+def _oracle_attention_for(base):
+    """fp32 windowed attention on the CPU (the same tile rule as the kernels),
+    window widths from the raw RoPE base `base`; q and k arrive rotated by HF."""
+    def attend(module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kw):
+        b, hq, L, d = query.shape
+        S = key.shape[-2]
+        qs, ks = OA.to_sorted(query.float().cpu()), OA.to_sorted(key.float().cpu())
+        vv = value.float().cpu()
+        w = WR.wavelengths_sorted(d, base, K_RET)
+        if L == 1:  # the hook decodes with the vec8 table, per-key rule (gates/g2_correctness.py:37-70)
+            z8 = WR.zhi_slice_vec8(d, base, K_RET)
+            out = torch.stack([OA.ref_decode_sliced(qs[bi, :, 0], ks[bi].transpose(0, 1), vv[bi].transpose(0, 1),
+                                                    z8, 8)[0] for bi in range(b)])[:, :, None, :]
+        else:
+            out = OA.ref_window_attn(qs, ks, vv, w, phase="prefill", block_m=32, block_n=32, q_offset=S - L)
+        return out.transpose(1, 2).contiguous().to(query.dtype).to(query.device), None
+    return attend
+
+
+_oracle_attention = _oracle_attention_for(BASE)
 
 
 def _logits(model, ids):
@@ -197,4 +209,69 @@ def test_generate_with_paged_cache_equals_dynamic_cache(dev):
     for a, b in zip(dyn.logits, paged.logits):
         assert torch.equal(a, b)
     assert cache.get_seq_length() == N + 5  # the last generated token is not fed back
+    hf.unregister(model)
+
+
+# ---- a second model family: Llama with llama3 RoPE scaling ----
+LLAMA_BASE = 5e5
+LLAMA_ROPE = {"rope_type": "llama3", "rope_theta": LLAMA_BASE, "factor": 8.0, "low_freq_factor": 1.0,
+              "high_freq_factor": 4.0, "original_max_position_embeddings": 8192}
+
+
+def _llama_model(dev):
+    from transformers import LlamaConfig, LlamaForCausalLM
+    cfg = LlamaConfig(vocab_size=512, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=16384,
+                      rope_parameters=dict(LLAMA_ROPE))
+    torch.manual_seed(0)
+    m = LlamaForCausalLM(cfg).to(torch.bfloat16).to(dev).eval()
+    m.set_attn_implementation("eager")
+    return m
+
+
+def test_llama3_scaled_rope_tables(dev):
+    """The hook's tables for the scaled model: widths from the raw base, RoPE at
+    load from the scaled inverse frequencies (which differ from the raw ones)."""
+    model = _llama_model(dev)
+    hook = hf.register(model, K_RET, K_RET, n_ctx=4096, mode="win")
+    assert hook.window.prefill_zhi == tuple(WR.window_zhi_from_kret(128, LLAMA_BASE, K_RET, 4096))
+    assert hook.window.decode_zhi8 == tuple(int(z) for z in WR.zhi_slice_vec8(128, LLAMA_BASE, K_RET))
+    raw = 1.0 / (LLAMA_BASE ** (torch.arange(0, 128, 2, dtype=torch.float64) / 128))
+    scaled = hook.window.inv_freq.double()
+    assert (scaled - raw).abs().gt(1e-3 * raw).sum().item() >= 30  # the llama3 rule rescales the long wavelengths
+    hf.unregister(model)
+
+
+def test_llama3_scaled_hook_off_equals_eager_and_on_equals_oracle(dev):
+    model = _llama_model(dev)
+    ids = torch.randint(0, 512, (1, N), generator=torch.Generator().manual_seed(6)).to(dev)
+    eager = _logits(model, ids)
+    AttentionInterface.register("atf_oracle", _oracle_attention_for(LLAMA_BASE))
+    model.set_attn_implementation("atf_oracle")
+    ref_pf = _logits(model, ids)
+    ref_dec = _decode_logits(model, ids)
+    hook = hf.register(model, K_RET, K_RET, n_ctx=4096, mode="off")
+    _close(_logits(model, ids), eager, "llama3-scaled, window off vs eager, prefill")
+    hook.mode = "win"
+    got_pf = _logits(model, ids)
+    _close(got_pf, ref_pf, "llama3-scaled, window on vs oracle, prefill")
+    _close(_decode_logits(model, ids), ref_dec, "llama3-scaled, window on vs oracle, decode step")
+    hook.mode = "off"
+    assert (_logits(model, ids) - got_pf).abs().max().item() > 0.05  # the window bites at this length
+    hf.unregister(model)
+
+
+@pytest.mark.parametrize("rope_at_load", [True, False])
+def test_llama3_scaled_paged_cache_equals_oracle(rope_at_load, dev):
+    model = _llama_model(dev)
+    steps = 4
+    ids = torch.randint(0, 512, (1, 640 + steps), generator=torch.Generator().manual_seed(7)).to(dev)
+    AttentionInterface.register("atf_oracle", _oracle_attention_for(LLAMA_BASE))
+    model.set_attn_implementation("atf_oracle")
+    ref_last, ref_dec = _oracle_steps(model, ids, steps)
+    hook = hf.register(model, K_RET, K_RET, n_ctx=4096, mode="win", rope_at_load=rope_at_load)
+    last, dec, cache = _paged_run(model, hook, ids, 128, steps, dev)
+    _close(last, ref_last, f"llama3-scaled paged cache, rope_at_load={rope_at_load}: prefill in 128-token chunks")
+    for i, (a, b) in enumerate(zip(dec, ref_dec)):
+        _close(a, b, f"llama3-scaled paged cache, rope_at_load={rope_at_load}: decode step {i}")
     hf.unregister(model)
