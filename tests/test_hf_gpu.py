@@ -13,13 +13,14 @@ random-init Qwen2 model (2 layers, head_dim 128, GQA 4/2, RoPE base 1e4).
   layer 0's cached keys;
 * both RoPE modes of the hook: RoPE at load (the kernels rotate Q and K) and
   HF's rotation (pre-rotated q and k);
-* a second model family with RoPE scaling: a random-init Llama with llama3
-  scaling (the Llama-3.1/3.2 form, base 5e5, 35 of the 64 frequency pairs
-  rescaled).  The hook rotates with the scaled inverse frequencies and takes
-  the window widths from the raw base, as the reference's integration does
-  (e2e_pipeline/atflash_e2e_fafi.py:138-172); the oracle model (HF's own
-  rotation, widths from the raw base) must agree for prefill, a decode step
-  and the paged cache.
+* RoPE scaling: a random-init Llama with llama3 scaling (the Llama-3.1/3.2
+  form, base 5e5, 35 of the 64 frequency pairs rescaled) and a Qwen2 with
+  YaRN (factor 4, 47 pairs rescaled, cos and sin multiplied by its magnitude
+  factor 1.1386).  The hook rotates with the scaled inverse frequencies (and
+  the magnitude factor) and takes the window widths from the raw base, as the
+  reference's integration does (e2e_pipeline/atflash_e2e_fafi.py:138-172);
+  the oracle model (HF's own rotation, widths from the raw base) must agree
+  for prefill, a decode step and the paged cache.
 """
 import pytest
 import torch
@@ -81,11 +82,18 @@ def _decode_logits(model, ids):
 
 
 def _close(a, b, what):
+    """Logits within bf16 noise: max and mean absolute difference, and, over many
+    positions, the same argmax almost everywhere.  (A single position's argmax
+    can flip on a near-tie of its top two logits, so one row is judged by the
+    differences alone.)"""
     d = (a - b).abs()
     agree = (a.argmax(-1) == b.argmax(-1)).float().mean().item()
+    rows = a.numel() // a.shape[-1]
     print(f"[hf hook] {what}: max {d.max().item():.3e} mean {d.mean().item():.3e} "
-          f"argmax agreement {agree:.3f} (logit scale {b.abs().max().item():.2f})", flush=True)
-    assert d.max().item() <= 0.1 and d.mean().item() <= 1e-2 and agree >= 0.95, what
+          f"argmax agreement {agree:.3f} over {rows} positions (logit scale {b.abs().max().item():.2f})", flush=True)
+    assert d.max().item() <= 0.1 and d.mean().item() <= 1e-2, what
+    if rows >= 20:
+        assert agree >= 0.95, what
 
 
 def test_hook_window_off_equals_eager(dev):
@@ -212,66 +220,78 @@ def test_generate_with_paged_cache_equals_dynamic_cache(dev):
     hf.unregister(model)
 
 
-# ---- a second model family: Llama with llama3 RoPE scaling ----
-LLAMA_BASE = 5e5
-LLAMA_ROPE = {"rope_type": "llama3", "rope_theta": LLAMA_BASE, "factor": 8.0, "low_freq_factor": 1.0,
-              "high_freq_factor": 4.0, "original_max_position_embeddings": 8192}
+# ---- RoPE scaling: llama3 on a Llama, YaRN on a Qwen2 ----
+# (raw base, rope_parameters, model family); llama3 rescales the long
+# wavelengths, YaRN also multiplies cos and sin by its magnitude factor
+# (attention_scaling 1.1386 here), which RoPE at load applies as HF does.
+SCALED = {
+    "llama3": (5e5, {"rope_type": "llama3", "rope_theta": 5e5, "factor": 8.0, "low_freq_factor": 1.0,
+                     "high_freq_factor": 4.0, "original_max_position_embeddings": 8192}, "llama"),
+    "yarn": (1e4, {"rope_type": "yarn", "rope_theta": 1e4, "factor": 4.0, "original_max_position_embeddings": 2048},
+             "qwen2"),
+}
 
 
-def _llama_model(dev):
+def _scaled_model(kind, dev):
     from transformers import LlamaConfig, LlamaForCausalLM
-    cfg = LlamaConfig(vocab_size=512, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
-                      num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=16384,
-                      rope_parameters=dict(LLAMA_ROPE))
+    base, rope, family = SCALED[kind]
+    Cfg, Model = (LlamaConfig, LlamaForCausalLM) if family == "llama" else (Qwen2Config, Qwen2ForCausalLM)
+    cfg = Cfg(vocab_size=512, hidden_size=512, intermediate_size=1024, num_hidden_layers=2, num_attention_heads=4,
+              num_key_value_heads=2, max_position_embeddings=16384, rope_parameters=dict(rope))
     torch.manual_seed(0)
-    m = LlamaForCausalLM(cfg).to(torch.bfloat16).to(dev).eval()
+    m = Model(cfg).to(torch.bfloat16).to(dev).eval()
     m.set_attn_implementation("eager")
-    return m
+    return m, base
 
 
-def test_llama3_scaled_rope_tables(dev):
-    """The hook's tables for the scaled model: widths from the raw base, RoPE at
+@pytest.mark.parametrize("kind", sorted(SCALED))
+def test_scaled_rope_tables(kind, dev):
+    """The hook's tables for a scaled model: widths from the raw base, RoPE at
     load from the scaled inverse frequencies (which differ from the raw ones)."""
-    model = _llama_model(dev)
+    model, base = _scaled_model(kind, dev)
     hook = hf.register(model, K_RET, K_RET, n_ctx=4096, mode="win")
-    assert hook.window.prefill_zhi == tuple(WR.window_zhi_from_kret(128, LLAMA_BASE, K_RET, 4096))
-    assert hook.window.decode_zhi8 == tuple(int(z) for z in WR.zhi_slice_vec8(128, LLAMA_BASE, K_RET))
-    raw = 1.0 / (LLAMA_BASE ** (torch.arange(0, 128, 2, dtype=torch.float64) / 128))
+    assert hook.window.prefill_zhi == tuple(WR.window_zhi_from_kret(128, base, K_RET, 4096))
+    assert hook.window.decode_zhi8 == tuple(int(z) for z in WR.zhi_slice_vec8(128, base, K_RET))
+    raw = 1.0 / (base ** (torch.arange(0, 128, 2, dtype=torch.float64) / 128))
     scaled = hook.window.inv_freq.double()
-    assert (scaled - raw).abs().gt(1e-3 * raw).sum().item() >= 30  # the llama3 rule rescales the long wavelengths
+    assert (scaled - raw).abs().gt(1e-3 * raw).sum().item() >= 30
+    assert (hook.window.attention_scaling > 1.1) == (kind == "yarn")
     hf.unregister(model)
 
 
-def test_llama3_scaled_hook_off_equals_eager_and_on_equals_oracle(dev):
-    model = _llama_model(dev)
+@pytest.mark.parametrize("kind", sorted(SCALED))
+def test_scaled_rope_hook_off_equals_eager_and_on_equals_oracle(kind, dev):
+    model, base = _scaled_model(kind, dev)
     ids = torch.randint(0, 512, (1, N), generator=torch.Generator().manual_seed(6)).to(dev)
     eager = _logits(model, ids)
-    AttentionInterface.register("atf_oracle", _oracle_attention_for(LLAMA_BASE))
+    AttentionInterface.register("atf_oracle", _oracle_attention_for(base))
     model.set_attn_implementation("atf_oracle")
     ref_pf = _logits(model, ids)
     ref_dec = _decode_logits(model, ids)
     hook = hf.register(model, K_RET, K_RET, n_ctx=4096, mode="off")
-    _close(_logits(model, ids), eager, "llama3-scaled, window off vs eager, prefill")
+    _close(_logits(model, ids), eager, f"{kind}-scaled, window off vs eager, prefill")
     hook.mode = "win"
     got_pf = _logits(model, ids)
-    _close(got_pf, ref_pf, "llama3-scaled, window on vs oracle, prefill")
-    _close(_decode_logits(model, ids), ref_dec, "llama3-scaled, window on vs oracle, decode step")
+    _close(got_pf, ref_pf, f"{kind}-scaled, window on vs oracle, prefill")
+    _close(_decode_logits(model, ids), ref_dec, f"{kind}-scaled, window on vs oracle, decode step")
     hook.mode = "off"
     assert (_logits(model, ids) - got_pf).abs().max().item() > 0.05  # the window bites at this length
     hf.unregister(model)
 
 
+@pytest.mark.parametrize("kind", sorted(SCALED))
 @pytest.mark.parametrize("rope_at_load", [True, False])
-def test_llama3_scaled_paged_cache_equals_oracle(rope_at_load, dev):
-    model = _llama_model(dev)
+def test_scaled_rope_paged_cache_equals_oracle(kind, rope_at_load, dev):
+    model, base = _scaled_model(kind, dev)
     steps = 4
     ids = torch.randint(0, 512, (1, 640 + steps), generator=torch.Generator().manual_seed(7)).to(dev)
-    AttentionInterface.register("atf_oracle", _oracle_attention_for(LLAMA_BASE))
+    AttentionInterface.register("atf_oracle", _oracle_attention_for(base))
     model.set_attn_implementation("atf_oracle")
     ref_last, ref_dec = _oracle_steps(model, ids, steps)
     hook = hf.register(model, K_RET, K_RET, n_ctx=4096, mode="win", rope_at_load=rope_at_load)
     last, dec, cache = _paged_run(model, hook, ids, 128, steps, dev)
-    _close(last, ref_last, f"llama3-scaled paged cache, rope_at_load={rope_at_load}: prefill in 128-token chunks")
+    what = f"{kind}-scaled paged cache, rope_at_load={rope_at_load}"
+    _close(last, ref_last, f"{what}: prefill in 128-token chunks")
     for i, (a, b) in enumerate(zip(dec, ref_dec)):
-        _close(a, b, f"llama3-scaled paged cache, rope_at_load={rope_at_load}: decode step {i}")
+        _close(a, b, f"{what}: decode step {i}")
     hf.unregister(model)
