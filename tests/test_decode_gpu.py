@@ -93,6 +93,49 @@ def test_batched_paged_decode_random_pages(dev):
             H.assert_close(out[b], ref, f"seq {b} len {lens[b]} window={'on' if z else 'off'}")
 
 
+def test_ragged_batch_with_empty_sequences(dev):
+    """A decode batch holding empty sequences (length 0, no pages: a padded
+    serving batch).  An empty sequence reads nothing (its page-table row holds
+    only invalid entries, whose buffer ranges are empty) and its output is
+    exactly zero; the other sequences match the oracle, window OFF, level table
+    and vec8 table."""
+    from atflash import atflash_window as AW, fiwin_common as FW, interface, rope as R
+    from atflash.cache import PagedKVCache
+    base, hq, hkv = 5e5, 24, 8
+    lens = [0, 700, 0, 5000]
+    B = len(lens)
+    cache = PagedKVCache(sum(-(-n // 16) for n in lens) + 5, hkv, dev)
+    cache._free = torch.randperm(len(cache._free), generator=torch.Generator().manual_seed(8)).tolist()
+    maxlen = max(lens)
+    rt = R.rope_table(maxlen, R.inv_freq(H.D, base, dev))
+    g = torch.Generator().manual_seed(98)
+    seqs = []
+    for b, n in enumerate(lens):
+        cache.add_sequence(b, n)
+        seqs.append((H.randn_bf16((1, n, hkv, H.D), g), H.randn_bf16((1, n, hkv, H.D), g)))
+    table = cache.page_table(list(range(B)))
+    for b, (k, v) in enumerate(seqs):
+        if lens[b]:
+            torch.ops.atflash.kv_write(cache.k, cache.v, k.to(dev), v.to(dev),
+                                       torch.zeros(1, dtype=torch.int32, device=dev), table[b:b + 1].contiguous(), rt, 0)
+    q = H.randn_bf16((B, hq, H.D), g)
+    seq_lens = torch.tensor(lens, dtype=torch.int32, device=dev)
+    tables = {"off": None, "level": AW.window_zhi_from_kret(H.D, base, 2.0, 1 << 20),
+              "vec8": FW.zhi_slice_vec8(H.D, base, 2.0).tolist()}
+    for name, z in tables.items():
+        print(f"[decode parity] batch {lens} with empty sequences, window {name}", flush=True)
+        out = interface.decode_paged(q.to(dev), cache, table, seq_lens, maxlen, zhi=z, rope=rt).cpu()
+        for b, (k, v) in enumerate(seqs):
+            if lens[b] == 0:
+                assert torch.equal(out[b], torch.zeros_like(out[b])), f"empty sequence {b}, window {name}"
+            elif name == "vec8":
+                H.assert_close(out[b], H.decode_oracle_vec8(q[b], k[0], v[0], base, list(z), rope=True),
+                               f"seq {b} len {lens[b]} window vec8")
+            else:
+                ref = H.decode_oracle(q[b], k[0], v[0], base, 2.0 if z else float("inf"), True)
+                H.assert_close(out[b], ref, f"seq {b} len {lens[b]} window {name}")
+
+
 def test_decode_off_equals_k_inf_bitwise(dev):
     from atflash import atflash_window as AW
     g = torch.Generator().manual_seed(5)
