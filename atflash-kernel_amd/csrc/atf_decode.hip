@@ -84,21 +84,20 @@ struct DecHot {
 // The slices page p reads and whether an older key of it reads fewer.  Page
 // rule (level table): 2 L(p) slices, L(p) = levels of the youngest key's age.
 // Per-key rule: the youngest key's slices, #{s : zhi8[s] >= age}; a slice
-// boundary falls inside the page when the oldest key's count differs.  Both
-// counts are straight-line scalar compares over the table (kernel-argument
-// SGPRs): 0.4 us per call faster at 128K than walking the slice boundaries
-// page by page with a loop, whose branches sat in front of every page load.
+// boundary falls inside the page when the oldest key's count differs.  Lane
+// s < 16 holds zhi8[s] (zc; the other lanes a limit no age meets), so each
+// count is one vector compare and the popcount of its ballot (the caller keeps
+// every lane active): against 16 scalar compares per count, -0.3 to -1.0 us per
+// call at 32K-128K (+0.5 us at Llama 32K), and those in turn were 0.4 us per
+// call faster at 128K than walking the slice boundaries page by page with a
+// loop, whose branches sat in front of every page load.
 template <bool kPerKey>
-__device__ __forceinline__ void page_slices(const DecodeArgs& a, int p, int N, int& ns, bool& mask) {
+__device__ __forceinline__ void page_slices(const DecodeArgs& a, int zc, int p, int N, int& ns, bool& mask) {
   const int z_young = (N - 1) - (p * kPage + kPage - 1);
   if constexpr (kPerKey) {
     const int z_old = z_young + kPage - 1;
-    int cy = 0, co = 0;
-#pragma unroll
-    for (int s = 0; s < kSlices; ++s) {
-      cy += (a.st.zhi[s] >= z_young) ? 1 : 0;
-      co += (a.st.zhi[s] >= z_old) ? 1 : 0;
-    }
+    const int cy = __builtin_popcountll(__builtin_amdgcn_ballot_w64(zc >= z_young));
+    const int co = __builtin_popcountll(__builtin_amdgcn_ballot_w64(zc >= z_old));
     ns = cy;
     mask = co != cy;
   } else {
@@ -201,6 +200,12 @@ void decode_kernel(const int32_t* page_table, const int32_t* seq_lens, const uin
   // path, so that each page is waited for with the later pages' loads still in
   // flight, measured slower.)
   PageRegs pr[kDecUnroll];
+  // per-key rule: lane s < 16 holds zhi8[s], the others a limit no age meets,
+  // so a page's slice counts are one compare and a ballot popcount each
+  int zc = INT32_MIN;
+#pragma unroll
+  for (int s = 0; s < kSlices && kPerKey; ++s)
+    if (lane == s) zc = a.st.zhi[s];
   // Straight-line code up to the first page loads (a page past the split gets
   // an empty buffer range: its loads return zeros without a memory request), so
   // the compiler reads every kernel argument they need in the first batch.
@@ -208,7 +213,7 @@ void decode_kernel(const int32_t* page_table, const int32_t* seq_lens, const uin
   for (int u = 0; u < kDecUnroll; ++u) {
     int ns;
     bool mask;
-    page_slices<kPerKey>(a, p_first + u, N, ns, mask);
+    page_slices<kPerKey>(a, zc, p_first + u, N, ns, mask);
     dec_load_page(hot, h, ent[u], p_first + u < p_end, p_first + u, ns, mask, lane, pr[u]);
   }
 #pragma unroll
@@ -282,7 +287,7 @@ void decode_kernel(const int32_t* page_table, const int32_t* seq_lens, const uin
       PageRef ref_n{0, false};
       if (reload) {
         int ns;
-        page_slices<kPerKey>(a, pn, N, ns, mask_n);
+        page_slices<kPerKey>(a, zc, pn, N, ns, mask_n);
         ref_n = page_ref(hot, h, ent[u], true);
         dec_load_k(hot, ref_n, ns, lane, r.k);
       }
