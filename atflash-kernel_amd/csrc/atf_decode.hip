@@ -308,16 +308,18 @@ void decode_kernel(const int32_t* page_table, const int32_t* seq_lens, const uin
         }
       }
       mx = quad_max(mx);
-      const float m_new = fmaxf(m_run, mx);
-      float alpha, msc;
-      if (m_new == NEG_INF) {
-        alpha = 1.f;
-        msc = 0.f;
-      } else {
-        alpha = fast_exp2((m_run - m_new) * c);
-        msc = m_new * c;
+      // Lazy reference max: m_run moves only where a score exceeds it by more
+      // than 8 (log2 units; the first finite score always does), so P <= 256
+      // and O and l are rescaled on few pages.
+      const bool grow = (mx - m_run) * c > 8.f;  // -inf - -inf = NaN: no
+      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+        const float alpha = !grow ? 1.f : (m_run == NEG_INF ? 0.f : fast_exp2((m_run - mx) * c));
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < 8; ++db) O[db] *= alpha;
+        m_run = grow ? mx : m_run;
       }
-      m_run = m_new;
+      const float msc = (m_run == NEG_INF) ? 0.f : m_run * c;
       float pv[4];
       float ls = 0.f;
 #pragma unroll
@@ -325,16 +327,14 @@ void decode_kernel(const int32_t* page_table, const int32_t* seq_lens, const uin
         pv[i] = fast_exp2(__builtin_fmaf(S[i], c, -msc));
         ls += pv[i];
       }
-      l_run = l_run * alpha + ls;
+      l_run += ls;
       u32x2 pk;
       pk[0] = pack_bf16x2(pv[0], pv[1]);
       pk[1] = pack_bf16x2(pv[2], pv[3]);
       const s16x4 pb = __builtin_bit_cast(s16x4, pk);
 #pragma unroll
-      for (int db = 0; db < 8; ++db) {
-        O[db] *= alpha;
+      for (int db = 0; db < 8; ++db)
         O[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, r.v[db]), pb, O[db], 0, 0, 0);
-      }
       if (reload) {
         dec_load_v(hot, ref_n, lane, r.v);
         r.n0 = pn * kPage;
