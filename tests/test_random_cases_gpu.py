@@ -9,7 +9,7 @@ up to 3000 on randomly permuted pages of one pool, the level table (page rule)
 or the vec8 table (per-key rule), window OFF included; a second decode draw
 takes contexts of 3000-60000 tokens and groups up to 16 (9 and 12 included),
 so that the split merge runs with many splits in both of its lane layouts
-(eight split groups per head for G <= 8, four above).  The draws are printed
+(sixteen split groups per head for G <= 8, eight above).  The draws are printed
 before each case runs."""
 import random
 
