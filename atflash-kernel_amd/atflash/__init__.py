@@ -8,6 +8,8 @@
     cache           paged KV cache in the kernels' slice-blocked layout
     ops             torch.library operators over the HIP C ABI
     interface       reference-shaped entry points (_flash_attn_fwd, decode)
+    fa4, flashinfer the reference's two kernel calls by name and meaning
+                    (sorted-pair inputs): swap the import, keep the call
     model_tables    window and RoPE tables from a model config (rope scaling
                     included) with the pair-order guard
     hf              transformers attention-interface hook
@@ -19,11 +21,11 @@ infrastructure and lives outside the package (oracle/ at the repository root).
 from . import atflash_window, fiwin_common, window_table
 
 __all__ = ["window_table", "atflash_window", "fiwin_common", "rope", "cache", "ops", "interface", "model_tables",
-           "hf"]
+           "hf", "fa4", "flashinfer"]
 
 
 def __getattr__(name):
-    if name in ("rope", "cache", "ops", "interface", "model_tables", "hf"):
+    if name in ("rope", "cache", "ops", "interface", "model_tables", "hf", "fa4", "flashinfer"):
         import importlib
         return importlib.import_module(f".{name}", __name__)
     raise AttributeError(name)

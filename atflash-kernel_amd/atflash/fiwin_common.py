@@ -5,6 +5,10 @@ zhi_slice_vec8  the FlashInfer port's per-8-dim-slice table: slice tx (pairs
 theory_s_vec8   mean fraction of K read under that table and the 2/(1+s) ceiling.
 decode_s        the same fraction for this build's decode kernel, which applies
                 the 16-dim level table per 16-token page (block_n = 16).
+build_atfwin_module, run_atfwin
+                the port's module builder and runner (fiwin_common.py:64-112)
+                over this build's decode (atflash.flashinfer; loaded on use, so
+                the tables above need no GPU).
 """
 import math
 
@@ -57,3 +61,10 @@ def decode_s_slices(n_ctx: int, zhi_slice, block_n: int = 16):
     s = read / float(len(z) * n_pages)
     return s, 2.0 / (1.0 + s)
 
+
+
+def __getattr__(name):
+    if name in ("build_atfwin_module", "run_atfwin"):
+        from . import flashinfer
+        return getattr(flashinfer, name)
+    raise AttributeError(name)
