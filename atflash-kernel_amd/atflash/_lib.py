@@ -15,7 +15,7 @@ import torch  # noqa: F401  (binds the HIP runtime first, see above)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libatflash_hip.so")
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 ATF_OK = 0
 ATF_ERR_INVALID = 1
@@ -45,19 +45,19 @@ _sz = ctypes.c_size_t
 SIGNATURES = {
     "atf_abi_version": (_i, []),
     "atf_last_error": (ctypes.c_char_p, []),
-    "atf_kv_write_bf16": (_i, [_p, _p, _i, _i, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64,
+    "atf_kv_write_bf16": (_i, [_p, _i, _i, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64,
                                _i, _i, _p, _p, _i, _p, _i, _i, _p]),
-    "atf_prefill_bf16": (_i, [_p, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _p, _i, _p, _i,
+    "atf_prefill_bf16": (_i, [_p, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _i, _p, _i,
                               _i, _i, _i, _i, _i, _i, _p, _f, _p, _i, _i, _p]),
     "atf_decode_workspace_bytes": (_sz, [_i, _i, _i, _i]),
-    "atf_decode_paged_bf16": (_i, [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i, _p, _i, _p,
+    "atf_decode_paged_bf16": (_i, [_p, _i64, _i64, _p, _i64, _i64, _p, _i, _p, _i, _p,
                                    _i, _i, _i, _i, _p, _f, _p, _i, _i, _p, _sz, _p]),
-    "atf_decode_paged_slices_bf16": (_i, [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i, _p, _i, _p,
+    "atf_decode_paged_slices_bf16": (_i, [_p, _i64, _i64, _p, _i64, _i64, _p, _i, _p, _i, _p,
                                           _i, _i, _i, _i, _p, _f, _p, _i, _i, _p, _sz, _p]),
-    "atf_decode_paged_bf16_noalloc": (_i, [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i, _p, _i, _p,
+    "atf_decode_paged_bf16_noalloc": (_i, [_p, _i64, _i64, _p, _i64, _i64, _p, _i, _p, _i, _p,
                                            _i, _i, _i, _i, _p, _f, _p, _i, _i, _p]),
     "atf_prefill_mfma_probe": (_i, [_p, _i, _i, _p]),
-    "atf_decode_stream_probe": (_i, [_p, _sz, _p, _p, _i, _p, _i, _p, _i, _i, _i, _p]),
+    "atf_decode_stream_probe": (_i, [_p, _sz, _p, _i, _p, _i, _p, _i, _i, _i, _p, _p]),
     "atf_prefill_tile_levels": (_i, [_p, _i, _i, _i, _p, _p]),
     "atf_decode_page_levels": (_i, [_p, _i, _i, _p, _p]),
 }
@@ -124,7 +124,12 @@ def zhi_array(zhi, n=LEVELS):
     return arr
 
 
-K_BLOCK_SHAPE = (SLICES, PAGE_SIZE, SLICE_DIMS)  # one (page, kv head) K block of the cache
+# The paged cache: one block of two halves per (page, kv head), V half first.
+HALF_ELEMS = SLICES * PAGE_SIZE * SLICE_DIMS  # 2048 bf16 = 4 KB
+KV_BLOCK_SHAPE = (2, HALF_ELEMS)              # [V half, K half]
+V_HALF, K_HALF = 0, 1
+V_BLOCK_SHAPE = (HEAD_DIM, PAGE_SIZE)          # the V half: V transposed
+K_BLOCK_SHAPE = (SLICES, PAGE_SIZE, SLICE_DIMS)  # the K half: slice-blocked
 
 
 def ptr(t):

@@ -57,6 +57,7 @@ except ImportError:  # pragma: no cover - the package works without transformers
 from . import _lib
 from . import interface as I
 from . import ops
+from .cache import k_half, new_kv_cache, v_half
 from .model_tables import ModelWindow, window_from_config
 
 ATTN_NAME = "atf_window"
@@ -82,10 +83,9 @@ class PagedLayer(CacheLayerMixin):
         n_pages = owner.batch * owner.pages_per_seq
         self.owner = owner
         self.layer_idx = layer_idx
-        self.k = torch.zeros((n_pages, owner.num_kv_heads, *_lib.K_BLOCK_SHAPE), dtype=torch.bfloat16,
-                             device=owner.device)
-        self.v = torch.zeros((n_pages, owner.num_kv_heads, _lib.HEAD_DIM, PAGE), dtype=torch.bfloat16,
-                             device=owner.device)
+        self.kv = new_kv_cache(n_pages, owner.num_kv_heads, owner.device)
+        self.k = k_half(self.kv)  # views of the two halves
+        self.v = v_half(self.kv)
         self.length = 0       # tokens written (every sequence of the batch has the same length)
         self.prev_length = 0  # length before the last update (the last chunk's first position)
         self.last_key = None  # the key tensor of the last update until the hook reads it (identity check)
@@ -114,7 +114,7 @@ class PagedLayer(CacheLayerMixin):
         if self.length + L > o.capacity:
             raise ValueError(f"PagedCache holds {o.capacity} tokens per sequence; "
                              f"{self.length} + {L} would not fit")
-        ops.kv_write(self.k, self.v, key_states.transpose(1, 2), value_states.transpose(1, 2),
+        ops.kv_write(self.kv, key_states.transpose(1, 2), value_states.transpose(1, 2),
                      o.start_positions(self.length), o.page_table, o.rope_cs, _lib.LAYOUT_HALF_SPLIT)
         self.prev_length = self.length
         self.length += L
@@ -317,11 +317,11 @@ class WindowAttention:
                 raise ValueError("the cache was made for the other RoPE mode of this hook")
             if L == 1:
                 zhi = list(self.window.decode_zhi8) if windowed else None
-                o = ops.decode_paged(query[:, :, 0, :], lyr.k, lyr.v, owner.page_table, owner.seq_lens(S), S, zhi,
+                o = ops.decode_paged(query[:, :, 0, :], lyr.kv, owner.page_table, owner.seq_lens(S), S, zhi,
                                      scale, owner.rope_cs, _lib.LAYOUT_HALF_SPLIT)
                 return o.view(b, 1, hq, d), None
             zhi = list(self.window.prefill_zhi) if windowed else None
-            o, _ = ops.prefill(query.transpose(1, 2), lyr.k, lyr.v, owner.page_table, S, lyr.prev_length, zhi, scale,
+            o, _ = ops.prefill(query.transpose(1, 2), lyr.kv, owner.page_table, S, lyr.prev_length, zhi, scale,
                                owner.rope_cs, _lib.LAYOUT_HALF_SPLIT)
             return o, None  # [b, L, hq, d]
         # any other cache: key/value hold the whole history [b, hkv, S, d]
@@ -333,10 +333,10 @@ class WindowAttention:
                           stacklevel=2)
         rt = self.rope_table(S, query.device)
         if L == 1:
-            kc, vc, table = I.pack_kv(key.transpose(1, 2), value.transpose(1, 2), rope=rt)
+            kvc, table = I.pack_kv(key.transpose(1, 2), value.transpose(1, 2), rope=rt)
             seq = torch.full((b,), S, dtype=torch.int32, device=query.device)
             zhi = list(self.window.decode_zhi8) if windowed else None
-            o = ops.decode_paged(query[:, :, 0, :], kc, vc, table, seq, S, zhi, scale, rt, 0)
+            o = ops.decode_paged(query[:, :, 0, :], kvc, table, seq, S, zhi, scale, rt, 0)
             return o.view(b, 1, hq, d), None
         zhi = self.window.prefill_zhi if windowed else None
         o, _ = I._flash_attn_fwd(query.transpose(1, 2), key.transpose(1, 2), value.transpose(1, 2), causal=True,

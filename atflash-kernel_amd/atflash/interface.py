@@ -60,15 +60,14 @@ _DECODE_TABLES = (_lib.LEVELS, _lib.SLICES)
 
 def pack_kv(k, v, rope=None, layout="half_split", start_pos=0):
     """Write contiguous-sequence k/v [B, N, Hkv, 128] into a fresh paged cache with
-    an identity page table.  Returns (k_cache, v_cache, page_table)."""
+    an identity page table.  Returns (kv_cache, page_table)."""
     B, N, Hkv, D = k.shape
     pages = -(-(int(start_pos) + N) // PAGE)
-    k_cache = torch.empty((B * pages, Hkv, *_lib.K_BLOCK_SHAPE), dtype=torch.bfloat16, device=k.device)
-    v_cache = torch.empty((B * pages, Hkv, D, PAGE), dtype=torch.bfloat16, device=k.device)
+    kv_cache = torch.empty((B * pages, Hkv, *_lib.KV_BLOCK_SHAPE), dtype=torch.bfloat16, device=k.device)
     page_table = torch.arange(B * pages, dtype=torch.int32, device=k.device).view(B, pages)
     starts = torch.full((B,), int(start_pos), dtype=torch.int32, device=k.device)
-    ops.kv_write(k_cache, v_cache, k, v, starts, page_table, rope, _layout_id(layout))
-    return k_cache, v_cache, page_table
+    ops.kv_write(kv_cache, k, v, starts, page_table, rope, _layout_id(layout))
+    return kv_cache, page_table
 
 
 def _flash_attn_fwd(q, k, v, causal=True, pack_gqa=None, atflash_window_zhi=None, softmax_scale=None,
@@ -87,9 +86,9 @@ def _flash_attn_fwd(q, k, v, causal=True, pack_gqa=None, atflash_window_zhi=None
     if Nq > Nk:
         raise ValueError(f"L>S invalid: Nq={Nq} Nk={Nk}")
     scale = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
-    k_cache, v_cache, table = pack_kv(k, v, rope=rope, layout=layout)
+    kv_cache, table = pack_kv(k, v, rope=rope, layout=layout)
     off = Nk - Nq if q_offset is None else int(q_offset)
-    return ops.prefill(q, k_cache, v_cache, table, Nk, off, _zhi_list(atflash_window_zhi), scale, rope,
+    return ops.prefill(q, kv_cache, table, Nk, off, _zhi_list(atflash_window_zhi), scale, rope,
                        _layout_id(layout))
 
 
@@ -105,21 +104,21 @@ def single_decode_with_kv_cache(q, k, v, maybe_zhi=None, sm_scale=None, kv_layou
         raise ValueError("kv_layout must be NHD or HND")
     N = k.shape[0]
     scale = 1.0 / math.sqrt(q.shape[-1]) if sm_scale is None else float(sm_scale)
-    k_cache, v_cache, table = pack_kv(k.unsqueeze(0), v.unsqueeze(0), rope=rope, layout=layout)
+    kv_cache, table = pack_kv(k.unsqueeze(0), v.unsqueeze(0), rope=rope, layout=layout)
     seq = torch.tensor([N], dtype=torch.int32, device=q.device)
-    o = ops.decode_paged(q.unsqueeze(0), k_cache, v_cache, table, seq, N, _zhi_list(maybe_zhi, _DECODE_TABLES), scale,
+    o = ops.decode_paged(q.unsqueeze(0), kv_cache, table, seq, N, _zhi_list(maybe_zhi, _DECODE_TABLES), scale,
                          rope, _layout_id(layout))
     return o[0]
 
 
 def prefill_paged(q, cache, page_table, nk, q_offset, zhi=None, sm_scale=None, rope=None, layout="half_split"):
     scale = 1.0 / math.sqrt(q.shape[-1]) if sm_scale is None else float(sm_scale)
-    return ops.prefill(q, cache.k, cache.v, page_table, int(nk), int(q_offset), _zhi_list(zhi), scale, rope,
+    return ops.prefill(q, cache.kv, page_table, int(nk), int(q_offset), _zhi_list(zhi), scale, rope,
                        _layout_id(layout))
 
 
 def decode_paged(q, cache, page_table, seq_lens, max_seq_len, zhi=None, sm_scale=None, rope=None,
                  layout="half_split"):
     scale = 1.0 / math.sqrt(q.shape[-1]) if sm_scale is None else float(sm_scale)
-    return ops.decode_paged(q, cache.k, cache.v, page_table, seq_lens, int(max_seq_len),
+    return ops.decode_paged(q, cache.kv, page_table, seq_lens, int(max_seq_len),
                             _zhi_list(zhi, _DECODE_TABLES), scale, rope, _layout_id(layout))

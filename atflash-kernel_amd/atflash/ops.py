@@ -1,10 +1,13 @@
 """torch.library operators over the C ABI (namespace `atflash`).
 
-    torch.ops.atflash.kv_write(k_cache, v_cache, k, v, start_pos, page_table, rope_cs, layout)
-    torch.ops.atflash.prefill(q, k_cache, v_cache, page_table, nk, q_offset, zhi, sm_scale,
+    torch.ops.atflash.kv_write(kv_cache, k, v, start_pos, page_table, rope_cs, layout)
+    torch.ops.atflash.prefill(q, kv_cache, page_table, nk, q_offset, zhi, sm_scale,
                               rope_cs, layout) -> (out, lse)
-    torch.ops.atflash.decode_paged(q, k_cache, v_cache, page_table, seq_lens, max_seq_len, zhi,
+    torch.ops.atflash.decode_paged(q, kv_cache, page_table, seq_lens, max_seq_len, zhi,
                                    sm_scale, rope_cs, layout) -> out
+
+kv_cache is the paged cache, bf16 [num_pages, num_kv_heads, 2, 2048]
+(atflash.cache: V half, then K half, per page and kv head).
 
 Each op checks shapes and dtypes, then calls the HIP library on the current
 stream of the tensors' device.  There is no CPU or PyTorch fallback: a CPU
@@ -33,13 +36,11 @@ def _need(cond, msg):
         raise ValueError(msg)
 
 
-def _check_cache(k_cache, v_cache):
-    _need(k_cache.dtype == torch.bfloat16 and v_cache.dtype == torch.bfloat16, "caches must be bf16")
-    _need(k_cache.dim() == 5 and tuple(k_cache.shape[2:]) == _lib.K_BLOCK_SHAPE,
-          "k_cache must be [num_pages, num_kv_heads, 16, 16, 8]")
-    _need(v_cache.shape == (k_cache.shape[0], k_cache.shape[1], _lib.HEAD_DIM, _lib.PAGE_SIZE),
-          "v_cache must be [num_pages, num_kv_heads, 128, 16]")
-    _need(k_cache.is_contiguous() and v_cache.is_contiguous(), "caches must be contiguous")
+def _check_cache(kv_cache):
+    _need(kv_cache.dtype == torch.bfloat16, "kv_cache must be bf16")
+    _need(kv_cache.dim() == 4 and tuple(kv_cache.shape[2:]) == _lib.KV_BLOCK_SHAPE,
+          "kv_cache must be [num_pages, num_kv_heads, 2, 2048]")
+    _need(kv_cache.is_contiguous(), "kv_cache must be contiguous")
 
 
 def _layout(layout: int) -> int:
@@ -55,17 +56,17 @@ def _rope(rope_cs):
     return rope_cs, rope_cs.shape[0]
 
 
-def kv_write(k_cache: torch.Tensor, v_cache: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+def kv_write(kv_cache: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
              start_pos: torch.Tensor, page_table: torch.Tensor, rope_cs: Optional[torch.Tensor],
              layout: int) -> None:
     """Write k/v [B, T, Hkv, 128] (token t of sequence b at absolute position
     start_pos[b] + t) into the paged cache, rotating K with rope_cs."""
-    _need_gpu(k_cache, v_cache, k, v, start_pos, page_table, rope_cs)
-    _check_cache(k_cache, v_cache)
+    _need_gpu(kv_cache, k, v, start_pos, page_table, rope_cs)
+    _check_cache(kv_cache)
     _need(k.dtype == torch.bfloat16 and v.dtype == torch.bfloat16, "k and v must be bf16")
     _need(k.dim() == 4 and k.shape == v.shape and k.shape[-1] == _lib.HEAD_DIM,
           "k and v must be [B, T, Hkv, 128] of equal shape")
-    _need(k.shape[2] == k_cache.shape[1], "k heads must equal the cache's kv heads")
+    _need(k.shape[2] == kv_cache.shape[1], "k heads must equal the cache's kv heads")
     _need(k.stride(-1) == 1 and v.stride(-1) == 1, "last dim of k and v must be contiguous")
     _need(start_pos.dtype == torch.int32 and start_pos.numel() == k.shape[0], "start_pos must be int32 [B]")
     _need(page_table.dtype == torch.int32 and page_table.dim() == 2 and page_table.shape[0] == k.shape[0]
@@ -73,29 +74,29 @@ def kv_write(k_cache: torch.Tensor, v_cache: torch.Tensor, k: torch.Tensor, v: t
     rope_cs, max_pos = _rope(rope_cs)
     L = _lib.lib()
     _lib.check(L.atf_kv_write_bf16(
-        _lib.ptr(k_cache), _lib.ptr(v_cache), k_cache.shape[0], k_cache.shape[1],
+        _lib.ptr(kv_cache), kv_cache.shape[0], kv_cache.shape[1],
         _lib.ptr(k), k.stride(0), k.stride(1), k.stride(2),
         _lib.ptr(v), v.stride(0), v.stride(1), v.stride(2),
         k.shape[0], k.shape[1], _lib.ptr(start_pos.contiguous()), _lib.ptr(page_table), page_table.shape[1],
         _lib.ptr(rope_cs), max_pos, _layout(layout), _lib.stream_of(k.device)))
 
 
-_kv_write_op = torch.library.custom_op("atflash::kv_write", kv_write, mutates_args=("k_cache", "v_cache"))
+_kv_write_op = torch.library.custom_op("atflash::kv_write", kv_write, mutates_args=("kv_cache",))
 
 
 @_kv_write_op.register_fake
-def _(k_cache, v_cache, k, v, start_pos, page_table, rope_cs, layout):
+def _(kv_cache, k, v, start_pos, page_table, rope_cs, layout):
     return None
 
 
-def prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, page_table: torch.Tensor,
+def prefill(q: torch.Tensor, kv_cache: torch.Tensor, page_table: torch.Tensor,
             nk: int, q_offset: int, zhi: Optional[List[int]], sm_scale: float,
             rope_cs: Optional[torch.Tensor], layout: int) -> Tuple[torch.Tensor, torch.Tensor]:
     """Windowed causal GQA prefill of q [B, Nq, Hq, 128] (absolute positions
     q_offset..q_offset+Nq-1) against nk cached keys.  Returns (out bf16
     [B, Nq, Hq, 128], lse fp32 [B, Hq, Nq])."""
-    _need_gpu(q, k_cache, v_cache, page_table, rope_cs)
-    _check_cache(k_cache, v_cache)
+    _need_gpu(q, kv_cache, page_table, rope_cs)
+    _check_cache(kv_cache)
     _need(q.dtype == torch.bfloat16 and q.dim() == 4 and q.shape[-1] == _lib.HEAD_DIM,
           "q must be bf16 [B, Nq, Hq, 128]")
     _need(q.stride(-1) == 1, "last dim of q must be contiguous")
@@ -109,8 +110,8 @@ def prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, page_
     _lib.check(L.atf_prefill_bf16(
         _lib.ptr(out), out.stride(0), out.stride(1), out.stride(2), _lib.ptr(lse),
         _lib.ptr(q), q.stride(0), q.stride(1), q.stride(2),
-        _lib.ptr(k_cache), _lib.ptr(v_cache), k_cache.shape[0], _lib.ptr(page_table), page_table.shape[1],
-        B, Nq, int(nk), int(q_offset), Hq, k_cache.shape[1], _lib.zhi_array(zhi), float(sm_scale),
+        _lib.ptr(kv_cache), kv_cache.shape[0], _lib.ptr(page_table), page_table.shape[1],
+        B, Nq, int(nk), int(q_offset), Hq, kv_cache.shape[1], _lib.zhi_array(zhi), float(sm_scale),
         _lib.ptr(rope_cs), max_pos, _layout(layout), _lib.stream_of(q.device)))
     return out, lse
 
@@ -119,7 +120,7 @@ _prefill_op = torch.library.custom_op("atflash::prefill", prefill, mutates_args=
 
 
 @_prefill_op.register_fake
-def _(q, k_cache, v_cache, page_table, nk, q_offset, zhi, sm_scale, rope_cs, layout):
+def _(q, kv_cache, page_table, nk, q_offset, zhi, sm_scale, rope_cs, layout):
     B, Nq, Hq, D = q.shape
     return q.new_empty((B, Nq, Hq, D)), q.new_empty((B, Hq, Nq), dtype=torch.float32)
 
@@ -148,15 +149,15 @@ def _decode_workspace(device, handle, B, hq, hkv, max_seq_len, L):
     return ws
 
 
-def decode_paged(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, page_table: torch.Tensor,
+def decode_paged(q: torch.Tensor, kv_cache: torch.Tensor, page_table: torch.Tensor,
                  seq_lens: torch.Tensor, max_seq_len: int, zhi: Optional[List[int]], sm_scale: float,
                  rope_cs: Optional[torch.Tensor], layout: int) -> torch.Tensor:
     """Windowed split-KV decode of q [B, Hq, 128] (query of sequence b at
     position seq_lens[b] - 1).  Returns out bf16 [B, Hq, 128].  zhi: the level
     table (8 entries, page rule) or the per-slice vec8 table (16 entries,
     per-key rule), None for window OFF."""
-    _need_gpu(q, k_cache, v_cache, page_table, seq_lens, rope_cs)
-    _check_cache(k_cache, v_cache)
+    _need_gpu(q, kv_cache, page_table, seq_lens, rope_cs)
+    _check_cache(kv_cache)
     _need(q.dtype == torch.bfloat16 and q.dim() == 3 and q.shape[-1] == _lib.HEAD_DIM,
           "q must be bf16 [B, Hq, 128]")
     q_sb, q_sh, q_sd = q.stride()
@@ -165,7 +166,7 @@ def decode_paged(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
     _need(seq_lens.dtype == torch.int32 and seq_lens.numel() == B, "seq_lens must be int32 [B]")
     _need(page_table.dtype == torch.int32 and page_table.dim() == 2 and page_table.shape[0] == B
           and page_table.is_contiguous(), "page_table must be contiguous int32 [B, max_pages]")
-    num_pages, hkv = k_cache.shape[0], k_cache.shape[1]
+    num_pages, hkv = kv_cache.shape[0], kv_cache.shape[1]
     rope_cs, max_pos = _rope(rope_cs)
     L = _lib.lib()
     dev = q.device
@@ -179,7 +180,7 @@ def decode_paged(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
         seq_lens = seq_lens.contiguous()
     _lib.check(entry(
         out.data_ptr(), Hq * _lib.HEAD_DIM, _lib.HEAD_DIM, q.data_ptr(), q_sb, q_sh,
-        k_cache.data_ptr(), v_cache.data_ptr(), num_pages, page_table.data_ptr(), page_table.shape[1],
+        kv_cache.data_ptr(), num_pages, page_table.data_ptr(), page_table.shape[1],
         seq_lens.data_ptr(), B, Hq, hkv, int(max_seq_len), table, float(sm_scale),
         _lib.ptr(rope_cs), max_pos, _layout(layout), ws[0], ws[1], stream))
     return out
@@ -189,7 +190,7 @@ _decode_paged_op = torch.library.custom_op("atflash::decode_paged", decode_paged
 
 
 @_decode_paged_op.register_fake
-def _(q, k_cache, v_cache, page_table, seq_lens, max_seq_len, zhi, sm_scale, rope_cs, layout):
+def _(q, kv_cache, page_table, seq_lens, max_seq_len, zhi, sm_scale, rope_cs, layout):
     return q.new_empty(q.shape)
 
 

@@ -136,25 +136,24 @@ int atf_abi_version(void) { return ATF_ABI_VERSION; }
 
 const char* atf_last_error(void) { return g_last_error.c_str(); }
 
-int atf_kv_write_bf16(void* k_cache, void* v_cache, int num_pages, int num_kv_heads, const void* k_src,
+int atf_kv_write_bf16(void* kv_cache, int num_pages, int num_kv_heads, const void* k_src,
                       int64_t ks_b, int64_t ks_t, int64_t ks_h, const void* v_src, int64_t vs_b, int64_t vs_t,
                       int64_t vs_h, int batch, int n_tokens, const int32_t* start_pos, const int32_t* page_table,
                       int max_pages, const float* rope_cs, int rope_max_pos, int layout, void* stream) {
   if (batch < 0 || n_tokens < 0) return fail(ATF_ERR_INVALID, "batch and n_tokens must be >= 0");
   if (batch == 0 || n_tokens == 0) return ok();
-  if (!k_cache || !v_cache || !k_src || !v_src || !start_pos || !page_table)
+  if (!kv_cache || !k_src || !v_src || !start_pos || !page_table)
     return fail(ATF_ERR_INVALID, "null pointer argument");
   if (num_pages <= 0 || num_kv_heads <= 0 || max_pages <= 0)
     return fail(ATF_ERR_INVALID, "num_pages, num_kv_heads and max_pages must be positive");
   if (int r = check_layout(layout, rope_cs, rope_max_pos)) return r;
-  if (!aligned(k_src, 16) || !aligned(v_src, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16))
-    return fail(ATF_ERR_INVALID, "k/v sources and caches must be 16-byte aligned");
+  if (!aligned(k_src, 16) || !aligned(v_src, 16) || !aligned(kv_cache, 16))
+    return fail(ATF_ERR_INVALID, "k/v sources and kv_cache must be 16-byte aligned");
   const int64_t strides[6] = {ks_b, ks_t, ks_h, vs_b, vs_t, vs_h};
   for (int64_t s : strides)
     if (s % 8 != 0) return fail(ATF_ERR_INVALID, "source strides must be multiples of 8 elements");
   atf::KvWriteArgs a{};
-  a.k_cache = static_cast<uint16_t*>(k_cache);
-  a.v_cache = static_cast<uint16_t*>(v_cache);
+  a.kv_cache = static_cast<uint16_t*>(kv_cache);
   a.num_pages = num_pages;
   a.hkv = num_kv_heads;
   a.k_src = static_cast<const uint16_t*>(k_src);
@@ -175,13 +174,13 @@ int atf_kv_write_bf16(void* k_cache, void* v_cache, int num_pages, int num_kv_he
 }
 
 int atf_prefill_bf16(void* out, int64_t o_sb, int64_t o_st, int64_t o_sh, float* lse, const void* q,
-                     int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k_cache, const void* v_cache,
+                     int64_t q_sb, int64_t q_st, int64_t q_sh, const void* kv_cache,
                      int num_pages, const int32_t* page_table, int max_pages, int batch, int nq, int nk,
                      int q_offset, int num_q_heads, int num_kv_heads, const int32_t* zhi, float sm_scale,
                      const float* rope_cs, int rope_max_pos, int layout, void* stream) {
   if (batch < 0 || nq < 0) return fail(ATF_ERR_INVALID, "batch and nq must be >= 0");
   if (batch == 0 || nq == 0) return ok();
-  if (!out || !q || !k_cache || !v_cache || !page_table) return fail(ATF_ERR_INVALID, "null pointer argument");
+  if (!out || !q || !kv_cache || !page_table) return fail(ATF_ERR_INVALID, "null pointer argument");
   if (num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0)
     return fail(ATF_ERR_INVALID, "num_q_heads (%d) must be a positive multiple of num_kv_heads (%d)", num_q_heads,
                 num_kv_heads);
@@ -195,8 +194,8 @@ int atf_prefill_bf16(void* out, int64_t o_sb, int64_t o_st, int64_t o_sh, float*
   if (int r = check_layout(layout, rope_cs, rope_max_pos)) return r;
   if (rope_cs && q_offset + nq > rope_max_pos)
     return fail(ATF_ERR_INVALID, "rope table has %d positions, need %d", rope_max_pos, q_offset + nq);
-  if (!aligned(q, 16) || !aligned(out, 8) || !aligned(k_cache, 16) || !aligned(v_cache, 16))
-    return fail(ATF_ERR_INVALID, "q, caches must be 16-byte and out 8-byte aligned");
+  if (!aligned(q, 16) || !aligned(out, 8) || !aligned(kv_cache, 16))
+    return fail(ATF_ERR_INVALID, "q and kv_cache must be 16-byte and out 8-byte aligned");
   if (q_sb % 8 || q_st % 8 || q_sh % 8) return fail(ATF_ERR_INVALID, "q strides must be multiples of 8 elements");
   if (o_sb % 4 || o_st % 4 || o_sh % 4) return fail(ATF_ERR_INVALID, "out strides must be multiples of 4 elements");
   atf::PrefillArgs a{};
@@ -206,8 +205,7 @@ int atf_prefill_bf16(void* out, int64_t o_sb, int64_t o_st, int64_t o_sh, float*
   a.out = static_cast<uint16_t*>(out);
   a.o_sb = o_sb; a.o_st = o_st; a.o_sh = o_sh;
   a.lse = lse;
-  a.k_cache = static_cast<const uint16_t*>(k_cache);
-  a.v_cache = static_cast<const uint16_t*>(v_cache);
+  a.kv_cache = static_cast<const uint16_t*>(kv_cache);
   a.num_pages = num_pages;
   a.page_table = page_table;
   a.max_pages = max_pages;
@@ -244,11 +242,11 @@ namespace {
 // Validation and argument packing shared by the two decode entry points
 // (everything except the workspace).
 int decode_prepare(void* out, int64_t o_sb, int64_t o_sh, const void* q, int64_t q_sb, int64_t q_sh,
-                   const void* k_cache, const void* v_cache, int num_pages, const int32_t* page_table, int max_pages,
+                   const void* kv_cache, int num_pages, const int32_t* page_table, int max_pages,
                    const int32_t* seq_lens, int batch, int num_q_heads, int num_kv_heads, int max_seq_len,
                    const int32_t* zhi, bool slice_table, float sm_scale, const float* rope_cs, int rope_max_pos,
                    int layout, atf::DecodeArgs* a) {
-  if (!out || !q || !k_cache || !v_cache || !page_table || !seq_lens)
+  if (!out || !q || !kv_cache || !page_table || !seq_lens)
     return fail(ATF_ERR_INVALID, "null pointer argument");
   if (num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0)
     return fail(ATF_ERR_INVALID, "num_q_heads (%d) must be a positive multiple of num_kv_heads (%d)", num_q_heads,
@@ -262,8 +260,8 @@ int decode_prepare(void* out, int64_t o_sb, int64_t o_sh, const void* q, int64_t
   if (int r = check_layout(layout, rope_cs, rope_max_pos)) return r;
   if (rope_cs && max_seq_len > rope_max_pos)
     return fail(ATF_ERR_INVALID, "rope table has %d positions, need %d", rope_max_pos, max_seq_len);
-  if (!aligned(q, 16) || !aligned(out, 8) || !aligned(k_cache, 16) || !aligned(v_cache, 16))
-    return fail(ATF_ERR_INVALID, "q, caches must be 16-byte and out 8-byte aligned");
+  if (!aligned(q, 16) || !aligned(out, 8) || !aligned(kv_cache, 16))
+    return fail(ATF_ERR_INVALID, "q and kv_cache must be 16-byte and out 8-byte aligned");
   if (q_sb % 8 || q_sh % 8) return fail(ATF_ERR_INVALID, "q strides must be multiples of 8 elements");
   if (o_sb % 4 || o_sh % 4) return fail(ATF_ERR_INVALID, "out strides must be multiples of 4 elements");
   if (int r = slice_table ? make_decode_table_slices(zhi, a)
@@ -275,8 +273,7 @@ int decode_prepare(void* out, int64_t o_sb, int64_t o_sh, const void* q, int64_t
   a->q = static_cast<const uint16_t*>(q);
   a->q_sb = q_sb;
   a->q_sh = q_sh;
-  a->k_cache = static_cast<const uint16_t*>(k_cache);
-  a->v_cache = static_cast<const uint16_t*>(v_cache);
+  a->kv_cache = static_cast<const uint16_t*>(kv_cache);
   a->num_pages = num_pages;
   a->page_table = page_table;
   a->max_pages = max_pages;
@@ -303,7 +300,7 @@ namespace {
 
 // Decode with a caller-provided workspace, either table kind.
 int decode_with_workspace(void* out, int64_t o_sb, int64_t o_sh, const void* q, int64_t q_sb, int64_t q_sh,
-                          const void* k_cache, const void* v_cache, int num_pages, const int32_t* page_table,
+                          const void* kv_cache, int num_pages, const int32_t* page_table,
                           int max_pages, const int32_t* seq_lens, int batch, int num_q_heads, int num_kv_heads,
                           int max_seq_len, const int32_t* zhi, bool slice_table, float sm_scale,
                           const float* rope_cs, int rope_max_pos, int layout, void* workspace,
@@ -311,7 +308,7 @@ int decode_with_workspace(void* out, int64_t o_sb, int64_t o_sh, const void* q, 
   if (batch < 0) return fail(ATF_ERR_INVALID, "batch must be >= 0");
   if (batch == 0) return ok();
   atf::DecodeArgs a{};
-  if (int r = decode_prepare(out, o_sb, o_sh, q, q_sb, q_sh, k_cache, v_cache, num_pages, page_table, max_pages,
+  if (int r = decode_prepare(out, o_sb, o_sh, q, q_sb, q_sh, kv_cache, num_pages, page_table, max_pages,
                              seq_lens, batch, num_q_heads, num_kv_heads, max_seq_len, zhi, slice_table, sm_scale,
                              rope_cs, rope_max_pos, layout, &a))
     return r;
@@ -332,35 +329,35 @@ int decode_with_workspace(void* out, int64_t o_sb, int64_t o_sh, const void* q, 
 extern "C" {
 
 int atf_decode_paged_bf16(void* out, int64_t o_sb, int64_t o_sh, const void* q, int64_t q_sb, int64_t q_sh,
-                          const void* k_cache, const void* v_cache, int num_pages, const int32_t* page_table,
+                          const void* kv_cache, int num_pages, const int32_t* page_table,
                           int max_pages, const int32_t* seq_lens, int batch, int num_q_heads, int num_kv_heads,
                           int max_seq_len, const int32_t* zhi, float sm_scale, const float* rope_cs,
                           int rope_max_pos, int layout, void* workspace, size_t workspace_bytes, void* stream) {
-  return decode_with_workspace(out, o_sb, o_sh, q, q_sb, q_sh, k_cache, v_cache, num_pages, page_table, max_pages,
+  return decode_with_workspace(out, o_sb, o_sh, q, q_sb, q_sh, kv_cache, num_pages, page_table, max_pages,
                                seq_lens, batch, num_q_heads, num_kv_heads, max_seq_len, zhi, false, sm_scale,
                                rope_cs, rope_max_pos, layout, workspace, workspace_bytes, stream);
 }
 
 int atf_decode_paged_slices_bf16(void* out, int64_t o_sb, int64_t o_sh, const void* q, int64_t q_sb, int64_t q_sh,
-                                 const void* k_cache, const void* v_cache, int num_pages, const int32_t* page_table,
+                                 const void* kv_cache, int num_pages, const int32_t* page_table,
                                  int max_pages, const int32_t* seq_lens, int batch, int num_q_heads,
                                  int num_kv_heads, int max_seq_len, const int32_t* zhi_slice, float sm_scale,
                                  const float* rope_cs, int rope_max_pos, int layout, void* workspace,
                                  size_t workspace_bytes, void* stream) {
-  return decode_with_workspace(out, o_sb, o_sh, q, q_sb, q_sh, k_cache, v_cache, num_pages, page_table, max_pages,
+  return decode_with_workspace(out, o_sb, o_sh, q, q_sb, q_sh, kv_cache, num_pages, page_table, max_pages,
                                seq_lens, batch, num_q_heads, num_kv_heads, max_seq_len, zhi_slice, true, sm_scale,
                                rope_cs, rope_max_pos, layout, workspace, workspace_bytes, stream);
 }
 
 int atf_decode_paged_bf16_noalloc(void* out, int64_t o_sb, int64_t o_sh, const void* q, int64_t q_sb, int64_t q_sh,
-                                  const void* k_cache, const void* v_cache, int num_pages,
+                                  const void* kv_cache, int num_pages,
                                   const int32_t* page_table, int max_pages, const int32_t* seq_lens, int batch,
                                   int num_q_heads, int num_kv_heads, int max_seq_len, const int32_t* zhi,
                                   float sm_scale, const float* rope_cs, int rope_max_pos, int layout, void* stream) {
   if (batch < 0) return fail(ATF_ERR_INVALID, "batch must be >= 0");
   if (batch == 0) return ok();
   atf::DecodeArgs a{};
-  if (int r = decode_prepare(out, o_sb, o_sh, q, q_sb, q_sh, k_cache, v_cache, num_pages, page_table, max_pages,
+  if (int r = decode_prepare(out, o_sb, o_sh, q, q_sb, q_sh, kv_cache, num_pages, page_table, max_pages,
                              seq_lens, batch, num_q_heads, num_kv_heads, max_seq_len, zhi, false, sm_scale,
                              rope_cs, rope_max_pos, layout, &a))
     return r;
@@ -400,21 +397,21 @@ int atf_prefill_mfma_probe(float* sink, int nq, int num_q_heads, void* stream) {
   return ok();
 }
 
-int atf_decode_stream_probe(uint32_t* sink, size_t sink_bytes, const void* k_cache, const void* v_cache,
+int atf_decode_stream_probe(uint32_t* sink, size_t sink_bytes, const void* kv_cache,
                             int num_pages, const int32_t* page_table, int max_pages, const int32_t* seq_lens,
-                            int batch, int num_kv_heads, int max_seq_len, void* stream) {
-  if (!sink || !k_cache || !v_cache || !page_table || !seq_lens) return fail(ATF_ERR_INVALID, "null pointer argument");
+                            int batch, int num_kv_heads, int max_seq_len, const int32_t* zhi_slice, void* stream) {
+  if (!sink || !kv_cache || !page_table || !seq_lens) return fail(ATF_ERR_INVALID, "null pointer argument");
   if (batch <= 0 || num_kv_heads <= 0 || max_seq_len <= 0 || max_seq_len >= (1 << 24) || num_pages <= 0 ||
       max_pages <= 0 || static_cast<int64_t>(max_pages) * atf::kPage < max_seq_len)
     return fail(ATF_ERR_INVALID, "bad arguments");
-  if (!aligned(k_cache, 16) || !aligned(v_cache, 16)) return fail(ATF_ERR_INVALID, "caches must be 16-byte aligned");
+  if (!aligned(kv_cache, 16)) return fail(ATF_ERR_INVALID, "kv_cache must be 16-byte aligned");
   atf::DecodeArgs a{};
+  if (int r = make_decode_table_slices(zhi_slice, &a)) return r;
   int ns = 1, pps = 1, waves = 0;
   decode_split(batch, num_kv_heads, max_seq_len, &ns, &pps, &waves);
   const size_t need = static_cast<size_t>(batch) * num_kv_heads * ns * atf::kDecWaves * sizeof(uint32_t);
   if (sink_bytes < need) return fail(ATF_ERR_WORKSPACE, "probe sink of %zu bytes required, got %zu", need, sink_bytes);
-  a.k_cache = static_cast<const uint16_t*>(k_cache);
-  a.v_cache = static_cast<const uint16_t*>(v_cache);
+  a.kv_cache = static_cast<const uint16_t*>(kv_cache);
   a.num_pages = num_pages;
   a.page_table = page_table;
   a.max_pages = max_pages;

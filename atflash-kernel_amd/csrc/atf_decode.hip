@@ -1,4 +1,5 @@
-// Windowed split-KV decode over the paged, slice-blocked KV cache (gfx950).
+// Windowed split-KV decode over the paged KV cache (gfx950): one block per
+// (page, kv head), the transposed V page and then the slice-blocked K page.
 //
 // Replaces the FlashInfer window port's single-request decode
 // (single_decode_with_kv_cache_with_jit_module(..., maybe_zhi_slice=...),
@@ -76,8 +77,7 @@ __device__ __forceinline__ int dec_fetch_entry(const int32_t* row, int p, int p_
 struct DecHot {
   const int32_t* page_table;
   const int32_t* seq_lens;
-  const uint16_t* k_cache;
-  const uint16_t* v_cache;
+  const uint16_t* kv_cache;
   int max_pages, pages_per_split, max_seq_len, hkv, num_pages;
 };
 
@@ -108,30 +108,32 @@ __device__ __forceinline__ void page_slices(const DecodeArgs& a, int zc, int p, 
 
 // K and V operands of page p whose page-table entry is `raw`, reading its first
 // ns slices of K; a page outside the split (in_split false) reads nothing.
-// The page's K and V blocks are range-checked buffer resources: a load at or
+// The page's V and K halves are range-checked buffer resources: a load at or
 // past the range returns zeros without a memory request.  K's slices are a
-// contiguous prefix of its block, so a range of ns * 256 bytes reads the
-// in-window slices and yields zeros for the others; an invalid page entry gets
-// an empty range.  The loads are therefore unconditional: wave-uniform base,
+// contiguous prefix of its half, so a range of ns * 256 bytes reads the
+// in-window slices and yields zeros for the others, and what the page reads is
+// one contiguous run (V, then those slices); an invalid page entry gets an
+// empty range.  The loads are therefore unconditional: wave-uniform base,
 // 32-bit lane offset, immediate row offset, no per-load address arithmetic.
 // Every page is read once per call, so the loads are non-temporal.
 // (The range goes through readfirstlane: the level count is uniform, but the
 // compiler may count it in a vector register, and a resource built from one
 // becomes a loop over lanes around every load.)
 struct PageRef {
-  size_t blk_elems;  // offset of the (page, kv head) block in either cache, in elements
+  size_t blk_elems;  // offset of the (page, kv head) block in the cache, in elements
   bool ok;
 };
 __device__ __forceinline__ PageRef page_ref(const DecHot& a, int h, int raw, bool in_split) {
   const int pg = __builtin_amdgcn_readfirstlane(raw);
   const bool ok = in_split && pg >= 0 && pg < a.num_pages;
-  return PageRef{(static_cast<size_t>(ok ? pg : 0) * a.hkv + h) * kBlockElems, ok};
+  return PageRef{(static_cast<size_t>(ok ? pg : 0) * a.hkv + h) * kKvBlockElems, ok};
 }
 // K: slice 4 lp + lane/16, token lane%16: quad lp is the 1 KB run at lp * 1024
 __device__ __forceinline__ void dec_load_k(const DecHot& a, const PageRef& pr, int ns, int lane, u32x4 (&k)[4]) {
   const int k_range = __builtin_amdgcn_readfirstlane(pr.ok ? ns * (kPage * kSliceDims * 2) : 0);
   const __amdgpu_buffer_rsrc_t rk =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.k_cache) + pr.blk_elems, 0, k_range, kBufferWord3);
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.kv_cache) + pr.blk_elems + kKHalfElems, 0, k_range,
+                                        kBufferWord3);
   const uint32_t koff = static_cast<uint32_t>(lane) << 4;
 #pragma unroll
   for (int lp = 0; lp < 4; ++lp)
@@ -140,7 +142,7 @@ __device__ __forceinline__ void dec_load_k(const DecHot& a, const PageRef& pr, i
 // V^T operand: d row 16*db + lane%16, tokens 4*(lane/16)..+3 -> stored slots.
 __device__ __forceinline__ void dec_load_v(const DecHot& a, const PageRef& pr, int lane, u32x2 (&v)[8]) {
   const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(a.v_cache) + pr.blk_elems, 0, pr.ok ? kBlockElems * 2 : 0, kBufferWord3);
+      const_cast<uint16_t*>(a.kv_cache) + pr.blk_elems, 0, pr.ok ? kBlockElems * 2 : 0, kBufferWord3);
   const int grp = lane >> 4;
   const int slot0 = 4 * ((grp == 1) ? 2 : (grp == 2 ? 1 : grp));
   const uint32_t voff = (static_cast<uint32_t>(lane & 15) << 5) + static_cast<uint32_t>(slot0) * 2u;
@@ -161,10 +163,9 @@ __device__ __forceinline__ void dec_load_page(const DecHot& a, int h, int raw, b
 // workgroup per CU) or 4 (short contexts: smaller splits over more CUs).
 template <bool kPerKey, int kWaves>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2)))
-void decode_kernel(const int32_t* page_table, const int32_t* seq_lens, const uint16_t* k_cache,
-                   const uint16_t* v_cache, int max_pages, int pages_per_split, int max_seq_len, int hkv,
-                   int num_pages, DecodeArgs a) {
-  const DecHot hot{page_table, seq_lens, k_cache, v_cache, max_pages, pages_per_split, max_seq_len, hkv, num_pages};
+void decode_kernel(const int32_t* page_table, const int32_t* seq_lens, const uint16_t* kv_cache, int max_pages,
+                   int pages_per_split, int max_seq_len, int hkv, int num_pages, DecodeArgs a) {
+  const DecHot hot{page_table, seq_lens, kv_cache, max_pages, pages_per_split, max_seq_len, hkv, num_pages};
   // wave partials
   __shared__ __attribute__((aligned(16))) float sh_o[kWaves * kDecMaxGroup * kD];
   __shared__ float sh_m[kWaves * kDecMaxGroup], sh_l[kWaves * kDecMaxGroup];
@@ -391,17 +392,18 @@ void decode_kernel(const int32_t* page_table, const int32_t* seq_lens, const uin
 }
 
 // ---- measurement probe: the streaming ceiling of the decode's page loads ----
-// decode_kernel's grid, waves, split rule (window OFF), page-table fetches and
-// page loads (the same range-checked, non-temporal buffer loads, the same
-// 4-page groups with the rolling reload), with the compute replaced by an
-// XOR of the loaded words, no LDS combine and no merge: what the memory
-// system delivers to this access pattern.  One word per wave goes to
+// decode_kernel's grid, waves, split rule, page-table fetches and page loads
+// (the same range-checked, non-temporal buffer loads of V and of the K slices
+// the page's youngest key reads under a.st, the same 4-page groups with the
+// rolling reload), with the compute replaced by an XOR of the loaded words, no
+// LDS combine and no merge: what the memory system delivers to this access
+// pattern.  One word per wave goes to
 // sink[((b * hkv + h) * n_splits + s) * kDecWaves + wave].
 __global__ __launch_bounds__(kDecWaves * 64) __attribute__((amdgpu_waves_per_eu(2)))
-void decode_stream_probe_kernel(const int32_t* page_table, const int32_t* seq_lens, const uint16_t* k_cache,
-                                const uint16_t* v_cache, int max_pages, int pages_per_split, int max_seq_len,
-                                int hkv, int num_pages, int n_splits, uint32_t* sink) {
-  const DecHot hot{page_table, seq_lens, k_cache, v_cache, max_pages, pages_per_split, max_seq_len, hkv, num_pages};
+void decode_stream_probe_kernel(const int32_t* page_table, const int32_t* seq_lens, const uint16_t* kv_cache,
+                                int max_pages, int pages_per_split, int max_seq_len, int hkv, int num_pages,
+                                int n_splits, uint32_t* sink, DecodeArgs a) {
+  const DecHot hot{page_table, seq_lens, kv_cache, max_pages, pages_per_split, max_seq_len, hkv, num_pages};
   const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -416,9 +418,17 @@ void decode_stream_probe_kernel(const int32_t* page_table, const int32_t* seq_le
   const int n_pages = (N + kPage - 1) / kPage;
   const int p_end = min(n_pages, p_begin + hot.pages_per_split);
   PageRegs pr[kDecUnroll];
+  int zc = INT32_MIN;
 #pragma unroll
-  for (int u = 0; u < kDecUnroll; ++u)
-    dec_load_page(hot, h, ent[u], p_first + u < p_end, p_first + u, kSlices, false, lane, pr[u]);
+  for (int sl = 0; sl < kSlices; ++sl)
+    if (lane == sl) zc = a.st.zhi[sl];
+#pragma unroll
+  for (int u = 0; u < kDecUnroll; ++u) {
+    int ns;
+    bool mask;
+    page_slices<true>(a, zc, p_first + u, N, ns, mask);
+    dec_load_page(hot, h, ent[u], p_first + u < p_end, p_first + u, ns, false, lane, pr[u]);
+  }
 #pragma unroll
   for (int u = 0; u < kDecUnroll; ++u) ent[u] = dec_fetch_entry(row, p_first + kStride + u, p_begin, p_end);
   uint32_t acc = 0;
@@ -433,7 +443,10 @@ void decode_stream_probe_kernel(const int32_t* page_table, const int32_t* seq_le
       for (int db = 0; db < 8; ++db) acc ^= r.v[db][0] ^ r.v[db][1];
       const int pn = p0 + kStride + u;
       if (pn < p_end) {
-        dec_load_page(hot, h, ent[u], true, pn, kSlices, false, lane, pr[u]);
+        int ns;
+        bool mask;
+        page_slices<true>(a, zc, pn, N, ns, mask);
+        dec_load_page(hot, h, ent[u], true, pn, ns, false, lane, pr[u]);
         ent[u] = dec_fetch_entry(row, pn + kStride, p_begin, p_end);
       }
     }
@@ -629,8 +642,8 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t s) {
   if (a.batch <= 0) return hipSuccess;
   const dim3 grid(a.n_splits, a.hkv, a.batch);
 #define ATF_DEC_LAUNCH(PK, W)                                                                                   \
-  hipLaunchKernelGGL((decode_kernel<PK, W>), grid, dim3(W * 64), 0, s, a.page_table, a.seq_lens, a.k_cache,     \
-                     a.v_cache, a.max_pages, a.pages_per_split, a.max_seq_len, a.hkv, a.num_pages, a)
+  hipLaunchKernelGGL((decode_kernel<PK, W>), grid, dim3(W * 64), 0, s, a.page_table, a.seq_lens, a.kv_cache,    \
+                     a.max_pages, a.pages_per_split, a.max_seq_len, a.hkv, a.num_pages, a)
   if (a.waves == 8) {
     if (a.per_key) ATF_DEC_LAUNCH(true, 8); else ATF_DEC_LAUNCH(false, 8);
   } else {
@@ -696,8 +709,8 @@ hipError_t launch_decode_noalloc(DecodeArgs a, hipStream_t s) {
 hipError_t launch_decode_stream_probe(const DecodeArgs& a, uint32_t* sink, hipStream_t s) {
   if (a.batch <= 0) return hipSuccess;
   hipLaunchKernelGGL(decode_stream_probe_kernel, dim3(a.n_splits, a.hkv, a.batch), dim3(kDecWaves * 64), 0, s,
-                     a.page_table, a.seq_lens, a.k_cache, a.v_cache, a.max_pages, a.pages_per_split, a.max_seq_len,
-                     a.hkv, a.num_pages, a.n_splits, sink);
+                     a.page_table, a.seq_lens, a.kv_cache, a.max_pages, a.pages_per_split, a.max_seq_len, a.hkv,
+                     a.num_pages, a.n_splits, sink, a);
   return hipGetLastError();
 }
 

@@ -1,5 +1,6 @@
-// Paged KV-cache writer: RoPE on K at write time, slice-blocked K pages and
-// transposed V pages (the cache format both attention kernels read).
+// Paged KV-cache writer: RoPE on K at write time, one block per (page, kv
+// head) holding the transposed V page and then the slice-blocked K page (the
+// cache format both attention kernels read).
 //
 // Replaces the reference's two steps around the cache: the RoPE + head-dim
 // permutation patch (e2e_pipeline/atflash_e2e_fafi.py:186-192) and the HF cache
@@ -45,7 +46,7 @@ __global__ __launch_bounds__(128) void kv_write_kernel(KvWriteArgs a) {
   const int s0 = static_cast<int>(lo - p0), s1 = static_cast<int>(hi - p0);
   const int pg = a.page_table[static_cast<int64_t>(b) * a.max_pages + pidx];
   if (pg < 0 || pg >= a.num_pages) return;
-  const size_t blk0 = static_cast<size_t>(pg) * a.hkv * kBlockElems;  // the page's block of head 0
+  const size_t blk0 = static_cast<size_t>(pg) * a.hkv * kKvBlockElems;  // the page's block of head 0
   const int t0 = static_cast<int>(p0 - start);  // source token of slot 0
 
   // K lane roles and the (cos, sin) of the lane's position and level, loaded once
@@ -83,7 +84,7 @@ __global__ __launch_bounds__(128) void kv_write_kernel(KvWriteArgs a) {
           const bool hs = a.layout == kLayoutHalfSplit;
           const u32x4 sa = hs ? u32x4{y1[2], y1[3], y2[2], y2[3]} : y1;
           const u32x4 sb = hs ? u32x4{y1[0], y1[1], y2[0], y2[1]} : y2;
-          uint16_t* kdst = a.k_cache + blk0 + static_cast<size_t>(h0 + j) * kBlockElems +
+          uint16_t* kdst = a.kv_cache + blk0 + static_cast<size_t>(h0 + j) * kKvBlockElems + kKHalfElems +
                            (2 * l) * (kPage * kSliceDims) + slot * kSliceDims;
           *reinterpret_cast<u32x4*>(kdst) = sa;
           *reinterpret_cast<u32x4*>(kdst + kPage * kSliceDims) = sb;
@@ -111,7 +112,7 @@ __global__ __launch_bounds__(128) void kv_write_kernel(KvWriteArgs a) {
 #pragma unroll
     for (int j = 0; j < kKvwHeads; ++j) {
       if (h0 + j >= a.hkv) break;
-      uint16_t* vdst = a.v_cache + blk0 + static_cast<size_t>(h0 + j) * kBlockElems + d * kPage;
+      uint16_t* vdst = a.kv_cache + blk0 + static_cast<size_t>(h0 + j) * kKvBlockElems + d * kPage;
       uint32_t w[8];  // the row's 16 slots as 8 packed pairs
       if (s0 == 0 && s1 == kPage) {
 #pragma unroll

@@ -25,8 +25,7 @@ constexpr int kDecMaxSplits = 256;
 constexpr size_t kDecScratchBytes = size_t(8) << 20;
 
 struct KvWriteArgs {
-  uint16_t* k_cache;
-  uint16_t* v_cache;
+  uint16_t* kv_cache;  // [num_pages][hkv][V half | K half]
   int num_pages, hkv;
   const uint16_t* k_src;
   const uint16_t* v_src;
@@ -46,8 +45,7 @@ struct PrefillArgs {
   uint16_t* out;
   int64_t o_sb, o_st, o_sh;
   float* lse;  // [B][Hq][nq] natural-log LSE, or null
-  const uint16_t* k_cache;
-  const uint16_t* v_cache;
+  const uint16_t* kv_cache;  // [num_pages][hkv][V half | K half]
   int num_pages;
   const int32_t* page_table;
   int max_pages;
@@ -65,8 +63,7 @@ struct DecodeArgs {
   int64_t q_sb, q_sh;
   uint16_t* out;  // [B][Hq][128] (strided)
   int64_t o_sb, o_sh;
-  const uint16_t* k_cache;
-  const uint16_t* v_cache;
+  const uint16_t* kv_cache;  // [num_pages][hkv][V half | K half]
   int num_pages;
   const int32_t* page_table;
   int max_pages;

@@ -185,8 +185,9 @@ __device__ __forceinline__ void zero_page(lds_u8* dst, int lane) {
   for (int i = 0; i < 4; ++i) *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(dst + i * 1024 + lane * 16) = z;
 }
 
-// Stage one 4 KB page into LDS at `dst`: K (whole 1 KB level pairs covering
-// the first L levels; an odd L also copies level L, which is not read) or V.
+// Stage one 4 KB page half into LDS at `dst`: K (whole 1 KB level pairs
+// covering the first L levels; an odd L also copies level L, which is not
+// read) or V.
 // `pg` is the page id (-1: missing page, zero-filled); `voff` is the lane's
 // chunk offset within a copied 1 KB row (k_copy_src or v_copy_src).
 __device__ __forceinline__ void pf_load_page(const PrefillArgs& a, int kvh, int pg, int L, bool is_v, lds_u8* dst,
@@ -195,8 +196,8 @@ __device__ __forceinline__ void pf_load_page(const PrefillArgs& a, int kvh, int 
     zero_page(dst, lane);
     return;
   }
-  const size_t blk = (static_cast<size_t>(pg) * a.hkv + kvh) * 4096;
-  const uint8_t* src = reinterpret_cast<const uint8_t*>(is_v ? a.v_cache : a.k_cache) + blk;
+  const size_t blk = (static_cast<size_t>(pg) * a.hkv + kvh) * (kKvBlockElems * 2);
+  const uint8_t* src = reinterpret_cast<const uint8_t*>(a.kv_cache) + blk + (is_v ? 0 : kKHalfElems * 2);
   lds_copy_page(src, is_v ? 4096u : static_cast<uint32_t>((L + 1) >> 1) * 1024u, voff, dst);
 }
 
@@ -568,11 +569,11 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
   // barrier ending its next MFMA phase (steps 2u+2 and 2u+3); both are first
   // read at step 2u+4.  The MFMA phase runs unconditionally (P = 0 when there
   // is nothing to add) so the accumulators stay in place.
-  // The copying group's cache at this kv head and the page stride, computed
-  // once (loop invariants).
-  const uint8_t* cbase =
-      reinterpret_cast<const uint8_t*>(copies_v ? a.v_cache : a.k_cache) + static_cast<size_t>(kvh) * 4096;
-  const uint32_t pstride = static_cast<uint32_t>(a.hkv) * 4096u;
+  // The copying group's half (V or K) of page 0's block at this kv head and
+  // the page stride, computed once (loop invariants).
+  const uint8_t* cbase = reinterpret_cast<const uint8_t*>(a.kv_cache) +
+                         static_cast<size_t>(kvh) * (kKvBlockElems * 2) + (copies_v ? 0 : kKHalfElems * 2);
+  const uint32_t pstride = static_cast<uint32_t>(a.hkv) * (kKvBlockElems * 2u);
   const int U = T2 >> 1;
   // Every load issued so far has landed before the loop, so the compiler's
   // wait counting inside the loop starts from nothing outstanding (it would

@@ -281,10 +281,10 @@ def bench_gpu(args):
         print(f"[bench] prefill {name}: {res['prefill'][name]['median_ms']:.3f} ms", flush=True)
 
     # ---- prefill attention kernel alone (roofline), on a pre-packed cache ----
-    kc, vc, table = interface.pack_kv(k, v, rope=rt)
+    kvc, table = interface.pack_kv(k, v, rope=rt)
     for name, zhi in (windows.items() if args.only in ("all", "prefill") else []):
         zl = None if zhi is None else list(zhi)
-        fn = lambda: ops.prefill(q, kc, vc, table, N, 0, zl, scale, rt, 0)  # noqa: E731
+        fn = lambda: ops.prefill(q, kvc, table, N, 0, zl, scale, rt, 0)  # noqa: E731
         for _ in range(max(1, args.warmup // 2)):
             fn()
         with ClockSampler() as cs:
@@ -293,7 +293,7 @@ def bench_gpu(args):
         clk = res["clocks"]["prefill_attn_" + name].get("gfxclk_mhz") or {}
         print(f"[bench] prefill attention kernel {name}: {res['prefill_attn'][name]['median_ms']:.3f} ms"
               + (f" (gfx clock median {clk['median']:.0f} MHz)" if clk else ""), flush=True)
-    del kc, vc, table
+    del kvc, table
 
     # ---- the MFMA ceiling of the prefill's structure (same grid and MFMA
     # stream, no softmax, no K/V staging), at the same shape ----
@@ -321,7 +321,7 @@ def bench_gpu(args):
         cache = PagedKVCache(n_pages, HKV, dev)
         perm = torch.randperm(n_pages, generator=torch.Generator().manual_seed(100 + c))
         tab = perm.to(torch.int32).view(1, -1).to(dev)
-        torch.ops.atflash.kv_write(cache.k, cache.v, k, v, torch.zeros(1, dtype=torch.int32, device=dev), tab,
+        torch.ops.atflash.kv_write(cache.kv, k, v, torch.zeros(1, dtype=torch.int32, device=dev), tab,
                                    rt, 0)
         caches.append(cache)
         tables.append(tab)
@@ -329,7 +329,7 @@ def bench_gpu(args):
     # first pool again, timed as one batch of back-to-back launches ----
     if args.only in ("all", "kv_write"):
         z0 = torch.zeros(1, dtype=torch.int32, device=dev)
-        fw = lambda: torch.ops.atflash.kv_write(caches[0].k, caches[0].v, k, v, z0, tables[0], rt, 0)  # noqa: E731
+        fw = lambda: torch.ops.atflash.kv_write(caches[0].kv, k, v, z0, tables[0], rt, 0)  # noqa: E731
         for _ in range(args.warmup):
             fw()
         with ClockSampler() as cs:
@@ -351,7 +351,7 @@ def bench_gpu(args):
         def fn():
             i = it[0] % copies
             it[0] += 1
-            return ops.decode_paged(qd, caches[i].k, caches[i].v, tables[i], seq, N, zl, scale, rt, 0)
+            return ops.decode_paged(qd, caches[i].kv, tables[i], seq, N, zl, scale, rt, 0)
         for _ in range(args.warmup * 10):
             fn()
         with ClockSampler() as cs:
@@ -366,23 +366,29 @@ def bench_gpu(args):
         print(f"[bench] decode {name}: {res['decode'][name]['batch_mean_ms'] * 1e3:.2f} us per call "
               f"(graph replay {res['decode'][name]['graph_mean_ms'] * 1e3:.2f} us)", flush=True)
     # ---- the streaming ceiling of the decode's page loads (same grid and
-    # loads, no compute, no merge), over the same rotated pools ----
+    # loads, no compute, no merge), over the same rotated pools: window OFF,
+    # and the bytes of the k=2 level table (as slices) and of the vec8 table ----
     if args.only in ("all", "decode"):
         from atflash import _lib
         sink = torch.empty(HKV * 256 * 8, dtype=torch.int32, device=dev)
-        it = [0]
+        res["decode_probe"] = {}
+        probe_tables = {"off": None, "k2": [int(z) for z in windows["k2"] for _ in range(2)],
+                        "k2_vec8": list(dec_windows["k2_vec8"])}
+        for name, st in probe_tables.items():
+            arr = _lib.zhi_array(st, _lib.SLICES)
+            it = [0]
 
-        def fp():
-            i = it[0] % copies
-            it[0] += 1
-            _lib.check(_lib.lib().atf_decode_stream_probe(
-                sink.data_ptr(), sink.numel() * 4, caches[i].k.data_ptr(), caches[i].v.data_ptr(), n_pages,
-                tables[i].data_ptr(), n_pages, seq.data_ptr(), 1, HKV, N, _lib.stream_of(dev)))
-        for _ in range(args.warmup * 10):
-            fp()
-        res["decode_probe"] = {"batch_mean_ms": _events_time_median(fp, args.steps * 40)}
-        print(f"[bench] decode streaming probe: {res['decode_probe']['batch_mean_ms'] * 1e3:.2f} us per call",
-              flush=True)
+            def fp():
+                i = it[0] % copies
+                it[0] += 1
+                _lib.check(_lib.lib().atf_decode_stream_probe(
+                    sink.data_ptr(), sink.numel() * 4, caches[i].kv.data_ptr(), n_pages, tables[i].data_ptr(),
+                    n_pages, seq.data_ptr(), 1, HKV, N, arr, _lib.stream_of(dev)))
+            for _ in range(args.warmup * 10):
+                fp()
+            res["decode_probe"][name] = {"batch_mean_ms": _events_time_median(fp, args.steps * 40)}
+            print(f"[bench] decode streaming probe {name}: "
+                  f"{res['decode_probe'][name]['batch_mean_ms'] * 1e3:.2f} us per call", flush=True)
     res["decode_pool_bytes"] = copies * n_pages * HKV * 8192
     return res
 
@@ -436,16 +442,16 @@ def bench_detail(steps=3):
         k = torch.randn((1, N, hkv, D), generator=g, device=dev).to(torch.bfloat16)
         v = torch.randn((1, N, hkv, D), generator=g, device=dev).to(torch.bfloat16)
         rt = R.rope_table(N, R.inv_freq(D, base, dev))
-        kc, vc, table = interface.pack_kv(k, v, rope=rt)
+        kvc, table = interface.pack_kv(k, v, rope=rt)
         r = {}
         for name, zhi in (("off", None), ("k2", list(AW.window_zhi_from_kret(D, base, 2.0, 1 << 23)))):
-            r[name + "_ms"] = med(lambda: ops.prefill(q, kc, vc, table, N, 0, zhi, D ** -0.5, rt, 0), steps)
+            r[name + "_ms"] = med(lambda: ops.prefill(q, kvc, table, N, 0, zhi, D ** -0.5, rt, 0), steps)
         r["on_over_off"] = r["off_ms"] / r["k2_ms"]
         r.update(_ref_ratio("llama_prefill_ms", N))
         out["llama_prefill"][N] = r
         print(f"[bench detail] llama prefill {N}: off {r['off_ms']:.2f} ms k2 {r['k2_ms']:.2f} ms "
               f"({r['on_over_off']:.3f}x; reference {r['reference_ratio']:.3f}x)", flush=True)
-        del q, k, v, kc, vc, table, rt
+        del q, k, v, kvc, table, rt
         torch.cuda.empty_cache()
 
     # ---- Llama-3.2-3B decode, batch 1 and 8 ----
@@ -463,7 +469,7 @@ def bench_detail(steps=3):
             for c in range(copies):
                 tab = perm[c * B * pages:(c + 1) * B * pages].view(B, pages).to(torch.int32).to(dev)
                 for b in range(B):
-                    torch.ops.atflash.kv_write(pool.k, pool.v, k, v, torch.zeros(1, dtype=torch.int32, device=dev),
+                    torch.ops.atflash.kv_write(pool.kv, k, v, torch.zeros(1, dtype=torch.int32, device=dev),
                                                tab[b:b + 1].contiguous(), rt, 0)
                 tables.append(tab)
             del k, v
@@ -476,7 +482,7 @@ def bench_detail(steps=3):
                 def fn():
                     t = tables[it[0] % copies]
                     it[0] += 1
-                    return ops.decode_paged(q, pool.k, pool.v, t, seq, N, zhi, D ** -0.5, rt, 0)
+                    return ops.decode_paged(q, pool.kv, t, seq, N, zhi, D ** -0.5, rt, 0)
                 for _ in range(10):
                     fn()
                 r[name + "_us"] = _events_time_median(fn, 40 * steps) * 1e3
@@ -501,13 +507,13 @@ def bench_detail(steps=3):
         k = torch.randn((1, N, HKV, D), generator=g, device=dev).to(torch.bfloat16)
         v = torch.randn((1, N, HKV, D), generator=g, device=dev).to(torch.bfloat16)
         rt = R.rope_table(N, R.inv_freq(D, BASE, dev))
-        kc, vc, table = interface.pack_kv(k, v, rope=rt)
+        kvc, table = interface.pack_kv(k, v, rope=rt)
         del k, v
         r = {}
         for name, zhi in (("off", None), ("k2", list(AW.window_zhi_from_kret(D, BASE, 2.0, 1 << 23)))):
             def fn():
                 for c0 in range(0, N, C):
-                    ops.prefill(q[:, c0:c0 + C], kc, vc, table, c0 + C, c0, zhi, D ** -0.5, rt, 0)
+                    ops.prefill(q[:, c0:c0 + C], kvc, table, c0 + C, c0, zhi, D ** -0.5, rt, 0)
             fn()
             r[name + "_ms"] = statistics.median(_events_time(fn, 2))
         r["on_over_off"] = r["off_ms"] / r["k2_ms"]
@@ -516,7 +522,7 @@ def bench_detail(steps=3):
         out["qwen_prefill_chunked"][N] = r
         print(f"[bench detail] qwen prefill {N // 1024}K in 8K chunks: off {r['off_ms']:.1f} ms k2 {r['k2_ms']:.1f} ms "
               f"({r['on_over_off']:.3f}x; reference {r['reference_ratio']:.3f}x)", flush=True)
-        del q, kc, vc, table, rt
+        del q, kvc, table, rt
         torch.cuda.empty_cache()
 
     # ---- Qwen2.5-7B decode at 512K (batch 1, permuted pages, one 2 GB pool) ----
@@ -529,7 +535,7 @@ def bench_detail(steps=3):
     for c0 in range(0, N, 131072):  # written in 128K pieces to bound the temporaries
         k = torch.randn((1, 131072, HKV, D), generator=g, device=dev).to(torch.bfloat16)
         v = torch.randn((1, 131072, HKV, D), generator=g, device=dev).to(torch.bfloat16)
-        torch.ops.atflash.kv_write(pool.k, pool.v, k, v, torch.full((1,), c0, dtype=torch.int32, device=dev), tab,
+        torch.ops.atflash.kv_write(pool.kv, k, v, torch.full((1,), c0, dtype=torch.int32, device=dev), tab,
                                    rt, 0)
         del k, v
     q = torch.randn((1, HQ, D), generator=g, device=dev).to(torch.bfloat16)
@@ -537,7 +543,7 @@ def bench_detail(steps=3):
     r = {"kv_pool_bytes": pages * HKV * 8192}
     for name, zhi in (("off", None), ("k2", list(AW.window_zhi_from_kret(D, BASE, 2.0, 1 << 23))),
                       ("k2_vec8", FW.zhi_slice_vec8(D, BASE, 2.0).tolist())):
-        fn = lambda: ops.decode_paged(q, pool.k, pool.v, tab, seq, N, zhi, D ** -0.5, rt, 0)  # noqa: E731
+        fn = lambda: ops.decode_paged(q, pool.kv, tab, seq, N, zhi, D ** -0.5, rt, 0)  # noqa: E731
         for _ in range(10):
             fn()
         r[name + "_us"] = _events_time_batch(fn, 20 * steps) * 1e3
@@ -634,14 +640,23 @@ def _probe_summary(res, flops_off):
 
 def _decode_probe_summary(res, N):
     """The decode's streaming probe beside the window-OFF call: its time per
-    call, its rate against 8 TB/s, and the call's time over the probe's."""
-    if "decode_probe" not in res or "off" not in res["decode"]:
+    call, its rate against 8 TB/s, and the call's time over the probe's; for
+    the windowed tables, the probe's time, its OFF / ON ratio (what the memory
+    system gives the window's bytes) and the call's ratio beside it."""
+    probes = res.get("decode_probe") or {}
+    if "off" not in probes or "off" not in res["decode"]:
         return None
-    t = res["decode_probe"]["batch_mean_ms"] * 1e-3
+    t = probes["off"]["batch_mean_ms"] * 1e-3
     nbytes = N * HKV * D * 2 * 2
-    return {"kernel": "atf::decode_stream_probe_kernel (the decode's grid and page loads; no compute, no merge)",
-            "us_per_launch": t * 1e6, "GBps": nbytes / t / 1e9, "frac": nbytes / t / PEAK_HBM,
-            "call_us_over_probe_us": res["decode"]["off"]["batch_mean_ms"] * 1e-3 / t}
+    out = {"kernel": "atf::decode_stream_probe_kernel (the decode's grid and page loads; no compute, no merge)",
+           "us_per_launch": t * 1e6, "GBps": nbytes / t / 1e9, "frac": nbytes / t / PEAK_HBM,
+           "call_us_over_probe_us": res["decode"]["off"]["batch_mean_ms"] * 1e-3 / t}
+    for name in ("k2", "k2_vec8"):
+        if name in probes and name in res["decode"]:
+            tw = probes[name]["batch_mean_ms"] * 1e-3
+            out[name] = {"us_per_launch": tw * 1e6, "probe_off_over_on": t / tw,
+                         "call_off_over_on": res["decode"]["off"]["batch_mean_ms"] / res["decode"][name]["batch_mean_ms"]}
+    return out
 
 
 def _frac_at_clock(frac, summary):

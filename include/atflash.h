@@ -23,13 +23,15 @@
  * (kernels/flashinfer_port/fiwin_common.py:35-47); level l is slices 2l, 2l+1.
  *
  * Paged KV cache (one layer): pages of ATF_PAGE_SIZE = 16 tokens.
- *   k_cache  bf16 [num_pages][num_kv_heads][16 slices][16 tokens][8 dims]
- *            (slice s: half-split dims [64-4(s+1), 64-4s) then the same + 64;
- *            sorted pair dims [8s, 8s+8))
- *   v_cache  bf16 [num_pages][num_kv_heads][128 dims][16 token slots]
+ *   kv_cache  bf16 [num_pages][num_kv_heads][2][2048]: one 8 KB block per
+ *             (page, kv head), 16-byte aligned,
+ *     [0]  V half: [128 dims][16 token slots] (V transposed)
+ *     [1]  K half: [16 slices][16 tokens][8 dims] (slice s: half-split dims
+ *          [64-4(s+1), 64-4s) then the same + 64; sorted pair dims [8s, 8s+8))
  * written by atf_kv_write_bf16 (RoPE applied to K there); page_table is int32
  * [batch][max_pages] of page ids.  Token slots of a page that were never written
- * may hold any finite value.
+ * may hold any finite value.  A windowed read of a page is one contiguous run:
+ * the V half and the in-window prefix of the K half.
  *
  * RoPE.  rope_cs, when not NULL, is fp32 [rope_max_pos][64][2] holding
  * (cos, sin) of position * inv_freq[r] (HF rotate-half convention); NULL means
@@ -46,7 +48,7 @@
 extern "C" {
 #endif
 
-#define ATF_ABI_VERSION 2
+#define ATF_ABI_VERSION 3
 #define ATF_HEAD_DIM 128
 #define ATF_LEVELS 8
 #define ATF_SLICES 16
@@ -88,7 +90,7 @@ const char* atf_last_error(void);
  * Replaces the reference's RoPE + head-dim permutation patch and HF cache append
  * (e2e_pipeline/atflash_e2e_fafi.py:186-192, 101-119).
  */
-int atf_kv_write_bf16(void* k_cache, void* v_cache, int num_pages, int num_kv_heads,
+int atf_kv_write_bf16(void* kv_cache, int num_pages, int num_kv_heads,
                       const void* k_src, int64_t ks_b, int64_t ks_t, int64_t ks_h,
                       const void* v_src, int64_t vs_b, int64_t vs_t, int64_t vs_h,
                       int batch, int n_tokens, const int32_t* start_pos,
@@ -110,7 +112,7 @@ int atf_kv_write_bf16(void* k_cache, void* v_cache, int num_pages, int num_kv_he
  */
 int atf_prefill_bf16(void* out, int64_t o_sb, int64_t o_st, int64_t o_sh, float* lse,
                      const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh,
-                     const void* k_cache, const void* v_cache, int num_pages,
+                     const void* kv_cache, int num_pages,
                      const int32_t* page_table, int max_pages,
                      int batch, int nq, int nk, int q_offset, int num_q_heads, int num_kv_heads,
                      const int32_t* zhi, float sm_scale, const float* rope_cs, int rope_max_pos,
@@ -142,7 +144,7 @@ size_t atf_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, 
  */
 int atf_decode_paged_bf16(void* out, int64_t o_sb, int64_t o_sh,
                           const void* q, int64_t q_sb, int64_t q_sh,
-                          const void* k_cache, const void* v_cache, int num_pages,
+                          const void* kv_cache, int num_pages,
                           const int32_t* page_table, int max_pages, const int32_t* seq_lens,
                           int batch, int num_q_heads, int num_kv_heads, int max_seq_len,
                           const int32_t* zhi, float sm_scale, const float* rope_cs, int rope_max_pos,
@@ -164,7 +166,7 @@ int atf_decode_paged_bf16(void* out, int64_t o_sb, int64_t o_sh,
  */
 int atf_decode_paged_slices_bf16(void* out, int64_t o_sb, int64_t o_sh,
                                  const void* q, int64_t q_sb, int64_t q_sh,
-                                 const void* k_cache, const void* v_cache, int num_pages,
+                                 const void* kv_cache, int num_pages,
                                  const int32_t* page_table, int max_pages, const int32_t* seq_lens,
                                  int batch, int num_q_heads, int num_kv_heads, int max_seq_len,
                                  const int32_t* zhi_slice, float sm_scale, const float* rope_cs,
@@ -189,7 +191,7 @@ int atf_decode_paged_slices_bf16(void* out, int64_t o_sb, int64_t o_sh,
  */
 int atf_decode_paged_bf16_noalloc(void* out, int64_t o_sb, int64_t o_sh,
                                   const void* q, int64_t q_sb, int64_t q_sh,
-                                  const void* k_cache, const void* v_cache, int num_pages,
+                                  const void* kv_cache, int num_pages,
                                   const int32_t* page_table, int max_pages, const int32_t* seq_lens,
                                   int batch, int num_q_heads, int num_kv_heads, int max_seq_len,
                                   const int32_t* zhi, float sm_scale, const float* rope_cs, int rope_max_pos,
@@ -208,20 +210,24 @@ int atf_decode_paged_bf16_noalloc(void* out, int64_t o_sb, int64_t o_sh,
 int atf_prefill_mfma_probe(float* sink, int nq, int num_q_heads, void* stream);
 
 /*
- * Measurement only; no counterpart in the reference.  Streams the pages a
- * window-OFF decode of this shape reads (the same split grid as
- * atf_decode_paged_bf16, always as 8-wave workgroups -- the decode's own
- * shape wherever its splits hold 32 pages or more, as at 128K -- the same
- * page-table fetches and range-checked non-temporal page loads in 4-page
- * groups) with the compute
- * replaced by an XOR of the loaded words, and no merge: the rate the memory
- * system gives this access pattern, for comparison with the decode call.
- * sink: device uint32, at least batch x num_kv_heads x n_splits x 8 words
- * (n_splits <= 256); ATF_ERR_WORKSPACE if sink_bytes is smaller.
+ * Measurement only; no counterpart in the reference.  Streams the bytes a
+ * decode of this shape reads (the same split grid as atf_decode_paged_bf16,
+ * always as 8-wave workgroups -- the decode's own shape wherever its splits
+ * hold 32 pages or more, as at 128K -- the same page-table fetches and
+ * range-checked non-temporal page loads in 4-page groups: V and the K slices
+ * that each page's youngest key reads under zhi_slice, a HOST int32
+ * [ATF_SLICES] table as in atf_decode_paged_slices_bf16, or NULL for window
+ * OFF; a level table reads the same bytes as the slice table holding each
+ * level's entry twice) with the compute replaced by an XOR of the loaded
+ * words, and no merge: the rate the memory system gives this access pattern,
+ * for comparison with the decode call.  sink: device uint32, at least
+ * batch x num_kv_heads x n_splits x 8 words (n_splits <= 256);
+ * ATF_ERR_WORKSPACE if sink_bytes is smaller.
  */
-int atf_decode_stream_probe(uint32_t* sink, size_t sink_bytes, const void* k_cache, const void* v_cache,
+int atf_decode_stream_probe(uint32_t* sink, size_t sink_bytes, const void* kv_cache,
                             int num_pages, const int32_t* page_table, int max_pages, const int32_t* seq_lens,
-                            int batch, int num_kv_heads, int max_seq_len, void* stream);
+                            int batch, int num_kv_heads, int max_seq_len, const int32_t* zhi_slice,
+                            void* stream);
 
 /*
  * Per-tile level counts (D_eff / 16) as the kernels compute them, for tests of

@@ -66,7 +66,7 @@ def _paged_decode(lens, hq, hkv, base, k_ret, dev, seed, vec8=False):
         seqs.append((k, v))
     table = cache.page_table(list(range(B)))
     for b, (k, v) in enumerate(seqs):
-        torch.ops.atflash.kv_write(cache.k, cache.v, k, v,
+        torch.ops.atflash.kv_write(cache.kv, k, v,
                                    torch.zeros(1, dtype=torch.int32, device=dev), table[b:b + 1].contiguous(), rt, 0)
     seqs = [(k.cpu(), v.cpu()) for k, v in seqs]
     g = torch.Generator().manual_seed(seed + 1)
@@ -162,7 +162,7 @@ def test_c4_qwen_chunked_prefill_8k_chunks_bitwise(N, k_ret, dev):
     outs = []
     for c0 in range(0, N, C):
         c1 = c0 + C
-        torch.ops.atflash.kv_write(cache.k, cache.v, k[:, c0:c1], v[:, c0:c1],
+        torch.ops.atflash.kv_write(cache.kv, k[:, c0:c1], v[:, c0:c1],
                                    torch.tensor([c0], dtype=torch.int32, device=dev), table, rt, 0)
         o, _ = interface.prefill_paged(q[:, c0:c1], cache, table, nk=c1, q_offset=c0, zhi=zhi, rope=rt)
         outs.append(o)

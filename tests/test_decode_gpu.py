@@ -82,7 +82,7 @@ def test_batched_paged_decode_random_pages(dev):
     table = cache.page_table(list(range(B)))
     for b, (k, v) in enumerate(seqs):
         tb = table[b:b + 1].contiguous()
-        torch.ops.atflash.kv_write(cache.k, cache.v, k.to(dev), v.to(dev),
+        torch.ops.atflash.kv_write(cache.kv, k.to(dev), v.to(dev),
                                    torch.zeros(1, dtype=torch.int32, device=dev), tb, rt, 0)
     q = H.randn_bf16((B, hq, H.D), g)
     seq_lens = torch.tensor(lens, dtype=torch.int32, device=dev)
@@ -116,7 +116,7 @@ def test_ragged_batch_with_empty_sequences(dev):
     table = cache.page_table(list(range(B)))
     for b, (k, v) in enumerate(seqs):
         if lens[b]:
-            torch.ops.atflash.kv_write(cache.k, cache.v, k.to(dev), v.to(dev),
+            torch.ops.atflash.kv_write(cache.kv, k.to(dev), v.to(dev),
                                        torch.zeros(1, dtype=torch.int32, device=dev), table[b:b + 1].contiguous(), rt, 0)
     q = H.randn_bf16((B, hq, H.D), g)
     seq_lens = torch.tensor(lens, dtype=torch.int32, device=dev)
@@ -213,7 +213,7 @@ def test_workspace_reuse_with_more_sequences_and_heads(dev):
             seqs.append((H.randn_bf16((1, n, hkv, H.D), g), H.randn_bf16((1, n, hkv, H.D), g)))
         table = cache.page_table(list(range(B)))
         for b, (k, v) in enumerate(seqs):
-            torch.ops.atflash.kv_write(cache.k, cache.v, k.to(dev), v.to(dev),
+            torch.ops.atflash.kv_write(cache.kv, k.to(dev), v.to(dev),
                                        torch.zeros(1, dtype=torch.int32, device=dev), table[b:b + 1].contiguous(),
                                        None, 0)
         q = H.randn_bf16((B, hq, H.D), g)

@@ -109,11 +109,11 @@ def test_vec8_batched_paged_decode_random_pages(dev):
         kvs.append((k, v))
     table = cache.page_table(list(range(len(lens))))
     for b, (k, v) in enumerate(kvs):
-        torch.ops.atflash.kv_write(cache.k, cache.v, k.to(dev), v.to(dev), torch.zeros(1, dtype=torch.int32,
+        torch.ops.atflash.kv_write(cache.kv, k.to(dev), v.to(dev), torch.zeros(1, dtype=torch.int32,
                                    device=dev), table[b:b + 1].contiguous(), rt, 0)
     q = H.randn_bf16((len(lens), hq, H.D), g)
     seq = torch.tensor(lens, dtype=torch.int32, device=dev)
-    out = ops.decode_paged(q.to(dev), cache.k, cache.v, table, seq, max(lens), zhi8, H.D ** -0.5, rt, 0).cpu()
+    out = ops.decode_paged(q.to(dev), cache.kv, table, seq, max(lens), zhi8, H.D ** -0.5, rt, 0).cpu()
     for b, (k, v) in enumerate(kvs):
         ref = H.decode_oracle_vec8(q[b], k[0], v[0], base, zhi8, rope=True)
         H.assert_close(out[b], ref, f"batch {b} len {lens[b]}")

@@ -22,8 +22,16 @@ def test_page_table_gives_each_sequence_its_own_pages():
     assert c.pages_per_seq == 7  # ceil(100 / 16)
     assert c.page_table.tolist() == [list(range(7)), list(range(7, 14))]
     assert len(c.layers) == 2
+    kv = c.layers[0].kv
+    assert tuple(kv.shape) == (14, 2, 2, 2048) and kv.is_contiguous()
     assert tuple(c.layers[0].k.shape) == (14, 2, 16, 16, 8)
     assert tuple(c.layers[0].v.shape) == (14, 2, 128, 16)
+    # k and v are views of the K and V halves of each (page, kv head) block
+    c.layers[0].k[3, 1, 2, 5, 6] = 1.0
+    c.layers[0].v[4, 0, 100, 7] = 2.0
+    flat = kv.view(-1)
+    assert (flat == 1.0).nonzero().flatten().tolist() == [((3 * 2 + 1) * 2 + 1) * 2048 + (2 * 16 + 5) * 8 + 6]
+    assert (flat == 2.0).nonzero().flatten().tolist() == [((4 * 2 + 0) * 2 + 0) * 2048 + 100 * 16 + 7]
 
 
 @pytest.mark.parametrize("arg,expect", [(30, 30), (0, 0), (50, 40), (40, 40), (-5, 35), (-40, 0), (-100, 0)])

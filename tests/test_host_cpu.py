@@ -180,7 +180,7 @@ def no_gpu():
 
 
 def _prefill(L, **kw):
-    a = dict(out=FAKE, o_sb=0, o_st=0, o_sh=0, lse=None, q=FAKE, q_sb=0, q_st=0, q_sh=0, k=FAKE, v=FAKE,
+    a = dict(out=FAKE, o_sb=0, o_st=0, o_sh=0, lse=None, q=FAKE, q_sb=0, q_st=0, q_sh=0, kv=FAKE,
              num_pages=8, table=FAKE, max_pages=8, batch=1, nq=64, nk=128, q_offset=64, hq=28, hkv=4,
              zhi=None, scale=0.088, rope=None, rope_max=0, layout=0, stream=None)
     a.update(kw)
@@ -190,7 +190,7 @@ def _prefill(L, **kw):
 def _decode(L, **kw):
     # 4096 tokens: several splits, so a workspace is required and the calls below
     # stop at validation (at the latest at the workspace check)
-    a = dict(out=FAKE, o_sb=0, o_sh=0, q=FAKE, q_sb=0, q_sh=0, k=FAKE, v=FAKE, num_pages=256, table=FAKE,
+    a = dict(out=FAKE, o_sb=0, o_sh=0, q=FAKE, q_sb=0, q_sh=0, kv=FAKE, num_pages=256, table=FAKE,
              max_pages=256, seq_lens=FAKE, batch=1, hq=28, hkv=4, max_seq_len=4096, zhi=None, scale=0.088,
              rope=None, rope_max=0, layout=0, ws=FAKE, ws_bytes=0, stream=None)
     a.update(kw)
@@ -222,7 +222,7 @@ def test_validation_status_codes(no_gpu):
     assert _decode(L, o_sh=2) == INV                                  # out stride not a multiple of 4
     assert _decode(L) == WS                                           # workspace too small
     assert b"workspace" in L.atf_last_error()
-    assert L.atf_kv_write_bf16(FAKE, FAKE, 8, 4, None, 0, 0, 0, FAKE, 0, 0, 0, 1, 16, FAKE, FAKE, 8, None, 0, 0,
+    assert L.atf_kv_write_bf16(FAKE, 8, 4, None, 0, 0, 0, FAKE, 0, 0, 0, 1, 16, FAKE, FAKE, 8, None, 0, 0,
                                None) == INV
     assert L.atf_prefill_tile_levels(FAKE, -1, 4, 0, None, None) == INV
     assert L.atf_decode_page_levels(None, 4, 64, None, None) == INV
@@ -233,7 +233,7 @@ def test_noalloc_decode_validates_like_the_workspace_entry_point(no_gpu):
     before any device work (the pointers are never used)."""
     _lib = _lib_or_skip()
     L = _lib.lib()
-    a = dict(out=FAKE, o_sb=0, o_sh=0, q=FAKE, q_sb=0, q_sh=0, k=FAKE, v=FAKE, num_pages=8, table=FAKE,
+    a = dict(out=FAKE, o_sb=0, o_sh=0, q=FAKE, q_sb=0, q_sh=0, kv=FAKE, num_pages=8, table=FAKE,
              max_pages=8, seq_lens=FAKE, batch=1, hq=4, hkv=1, max_seq_len=0, zhi=None, scale=0.088,
              rope=None, rope_max=0, layout=0, stream=None)
     assert L.atf_decode_paged_bf16_noalloc(*a.values()) == _lib.ATF_ERR_INVALID   # max_seq_len 0
@@ -251,7 +251,7 @@ def test_slice_table_decode_validation(no_gpu):
     from atflash import fiwin_common as FW
     _lib = _lib_or_skip()
     L = _lib.lib()
-    a = dict(out=FAKE, o_sb=0, o_sh=0, q=FAKE, q_sb=0, q_sh=0, k=FAKE, v=FAKE, num_pages=256, table=FAKE,
+    a = dict(out=FAKE, o_sb=0, o_sh=0, q=FAKE, q_sb=0, q_sh=0, kv=FAKE, num_pages=256, table=FAKE,
              max_pages=256, seq_lens=FAKE, batch=1, hq=28, hkv=4, max_seq_len=4096, zhi=None, scale=0.088,
              rope=None, rope_max=0, layout=0, ws=FAKE, ws_bytes=0, stream=None)
 
@@ -321,22 +321,21 @@ def test_registered_ops_and_direct_functions_agree():
     the package calls directly are the same operations: both are registered
     or defined, take the same arguments and refuse CPU tensors alike."""
     from atflash import _lib, ops
-    kc = torch.zeros((2, 1, *_lib.K_BLOCK_SHAPE), dtype=torch.bfloat16)
-    vc = torch.zeros((2, 1, 128, 16), dtype=torch.bfloat16)
+    kvc = torch.zeros((2, 1, *_lib.KV_BLOCK_SHAPE), dtype=torch.bfloat16)
     q = torch.zeros((1, 4, 128), dtype=torch.bfloat16)
     table = torch.zeros((1, 2), dtype=torch.int32)
     seq = torch.full((1,), 20, dtype=torch.int32)
     for fn in (ops.decode_paged, torch.ops.atflash.decode_paged):
         with pytest.raises(ValueError, match="GPU"):
-            fn(q, kc, vc, table, seq, 20, [5] * 16, 0.1, None, 0)
+            fn(q, kvc, table, seq, 20, [5] * 16, 0.1, None, 0)
     qp = torch.zeros((1, 32, 4, 128), dtype=torch.bfloat16)
     for fn in (ops.prefill, torch.ops.atflash.prefill):
         with pytest.raises(ValueError, match="GPU"):
-            fn(qp, kc, vc, table, 32, 0, None, 0.1, None, 0)
+            fn(qp, kvc, table, 32, 0, None, 0.1, None, 0)
     kv = torch.zeros((1, 32, 1, 128), dtype=torch.bfloat16)
     for fn in (ops.kv_write, torch.ops.atflash.kv_write):
         with pytest.raises(ValueError, match="GPU"):
-            fn(kc, vc, kv, kv, torch.zeros(1, dtype=torch.int32), table, None, 0)
+            fn(kvc, kv, kv, torch.zeros(1, dtype=torch.int32), table, None, 0)
     # the window table arrays are built once per table and reused
     assert _lib.zhi_array([7] * 16, _lib.SLICES) is _lib.zhi_array(tuple([7] * 16), _lib.SLICES)
     assert list(_lib.zhi_array([9] * 8)) == [9] * 8

@@ -4,9 +4,17 @@ import pytest
 import torch
 
 import atflash.ops  # noqa: F401  (registers torch.ops.atflash)
+from atflash.cache import k_half
 import helpers as H
 
 pytestmark = pytest.mark.gpu
+
+
+def _assemble(ek, ev):
+    """The cache tensor holding the model's pages: per (page, kv head) an 8 KB
+    block, the V half [128 dims, 16 slots] first, then the K half
+    [16 slices, 16 tokens, 8 dims]."""
+    return torch.stack([ev.flatten(2), ek.flatten(2)], dim=2)
 
 
 def _expected_pages(k, v, table, start, n_pages_pool, hkv, layout=0, init=None):
@@ -48,14 +56,12 @@ def test_cache_layout_bit_exact(layout, hkv, dev):
     k = H.randn_bf16((n, hkv, H.D), g)
     v = H.randn_bf16((n, hkv, H.D), g)
     table = torch.randperm(pool, generator=g)[:-(-(start + n) // 16)].to(torch.int32)
-    kc = torch.zeros((pool, hkv, 16, 16, 8), dtype=torch.bfloat16, device=dev)
-    vc = torch.zeros((pool, hkv, 128, 16), dtype=torch.bfloat16, device=dev)
-    torch.ops.atflash.kv_write(kc, vc, k[None].to(dev), v[None].to(dev),
+    kv = torch.zeros((pool, hkv, 2, 2048), dtype=torch.bfloat16, device=dev)
+    torch.ops.atflash.kv_write(kv, k[None].to(dev), v[None].to(dev),
                                torch.tensor([start], dtype=torch.int32, device=dev),
                                table[None].to(dev).contiguous(), None, layout)
     ek, ev = _expected_pages(k, v, table.tolist(), start, pool, hkv, layout)
-    assert torch.equal(kc.cpu(), ek)
-    assert torch.equal(vc.cpu(), ev)
+    assert torch.equal(kv.cpu(), _assemble(ek, ev))
 
 
 def test_rope_at_write_matches_fp32_rotation(dev):
@@ -65,14 +71,14 @@ def test_rope_at_write_matches_fp32_rotation(dev):
     k = H.randn_bf16((n, hkv, H.D), g)
     v = H.randn_bf16((n, hkv, H.D), g)
     table = torch.arange(-(-n // 16), dtype=torch.int32)
-    kc = torch.zeros((len(table), hkv, 16, 16, 8), dtype=torch.bfloat16, device=dev)
-    vc = torch.zeros((len(table), hkv, 128, 16), dtype=torch.bfloat16, device=dev)
+    kv = torch.zeros((len(table), hkv, 2, 2048), dtype=torch.bfloat16, device=dev)
     rt = R.rope_table(n, R.inv_freq(H.D, base, dev))
-    torch.ops.atflash.kv_write(kc, vc, k[None].to(dev), v[None].to(dev),
+    torch.ops.atflash.kv_write(kv, k[None].to(dev), v[None].to(dev),
                                torch.zeros(1, dtype=torch.int32, device=dev), table[None].to(dev), rt, 0)
     kr = H.rotate(k[None], torch.arange(n), base)[0]       # fp32 oracle rotation
-    ek, _ = _expected_pages(kr, v, table.tolist(), 0, len(table), hkv)  # cast to bf16 inside
-    got = kc.cpu().float()
+    ek, ev = _expected_pages(kr, v, table.tolist(), 0, len(table), hkv)  # cast to bf16 inside
+    assert torch.equal(kv.cpu()[:, :, 0], ev.flatten(2))  # V is not rotated
+    got = k_half(kv).cpu().float()
     want = ek.float()
     # one bf16 rounding (2^-8 relative, allow 2^-7) plus an absolute floor for
     # rotated values that cancel to ~0, where the GPU and CPU cos/sin (each
@@ -84,6 +90,7 @@ def test_rope_at_write_matches_fp32_rotation(dev):
 
 
 def _random_cache(pool, hkv, g):
+    """(K pages, V pages) of random content, in the model's shapes."""
     return (H.randn_bf16((pool, hkv, 16, 16, 8), g), H.randn_bf16((pool, hkv, 128, 16), g))
 
 
@@ -96,12 +103,11 @@ def test_partial_pages_keep_the_other_slots(dev):
     k = H.randn_bf16((n, hkv, H.D), g)
     v = H.randn_bf16((n, hkv, H.D), g)
     table = torch.randperm(pool, generator=g)[:5].to(torch.int32)
-    kc, vc = init[0].to(dev), init[1].to(dev)
-    torch.ops.atflash.kv_write(kc, vc, k[None].to(dev), v[None].to(dev),
+    kv = _assemble(*init).to(dev)
+    torch.ops.atflash.kv_write(kv, k[None].to(dev), v[None].to(dev),
                                torch.tensor([start], dtype=torch.int32, device=dev), table[None].to(dev), None, 0)
     ek, ev = _expected_pages(k, v, table.tolist(), start, pool, hkv, init=init)
-    assert torch.equal(kc.cpu(), ek)
-    assert torch.equal(vc.cpu(), ev)
+    assert torch.equal(kv.cpu(), _assemble(ek, ev))
 
 
 def test_token_by_token_append_equals_one_write(dev):
@@ -113,14 +119,13 @@ def test_token_by_token_append_equals_one_write(dev):
     v = H.randn_bf16((n, hkv, H.D), g).to(dev)
     table = torch.randperm(pool, generator=g)[:4].to(torch.int32)[None].to(dev)
     init = _random_cache(pool, hkv, g)
-    a = (init[0].to(dev), init[1].to(dev))
-    b = (init[0].to(dev), init[1].to(dev))
-    torch.ops.atflash.kv_write(a[0], a[1], k[None], v[None], torch.zeros(1, dtype=torch.int32, device=dev), table,
-                               None, 0)
+    a = _assemble(*init).to(dev)
+    b = _assemble(*init).to(dev)
+    torch.ops.atflash.kv_write(a, k[None], v[None], torch.zeros(1, dtype=torch.int32, device=dev), table, None, 0)
     for t in range(n):
-        torch.ops.atflash.kv_write(b[0], b[1], k[None, t:t + 1], v[None, t:t + 1],
+        torch.ops.atflash.kv_write(b, k[None, t:t + 1], v[None, t:t + 1],
                                    torch.tensor([t], dtype=torch.int32, device=dev), table, None, 0)
-    assert torch.equal(a[0].cpu(), b[0].cpu()) and torch.equal(a[1].cpu(), b[1].cpu())
+    assert torch.equal(a.cpu(), b.cpu())
 
 
 def test_batch_with_a_negative_start(dev):
@@ -134,10 +139,9 @@ def test_batch_with_a_negative_start(dev):
     perm = torch.randperm(pool, generator=g).to(torch.int32)
     tables = torch.stack([perm[:4], perm[4:8]])
     starts = [5, -7]
-    kc, vc = init[0].to(dev), init[1].to(dev)
-    torch.ops.atflash.kv_write(kc, vc, k.to(dev), v.to(dev), torch.tensor(starts, dtype=torch.int32, device=dev),
+    kv = _assemble(*init).to(dev)
+    torch.ops.atflash.kv_write(kv, k.to(dev), v.to(dev), torch.tensor(starts, dtype=torch.int32, device=dev),
                                tables.to(dev).contiguous(), None, 0)
     ek, ev = _expected_pages(k[0], v[0], tables[0].tolist(), starts[0], pool, hkv, init=init)
     ek, ev = _expected_pages(k[1], v[1], tables[1].tolist(), starts[1], pool, hkv, init=(ek, ev))
-    assert torch.equal(kc.cpu(), ek)
-    assert torch.equal(vc.cpu(), ev)
+    assert torch.equal(kv.cpu(), _assemble(ek, ev))

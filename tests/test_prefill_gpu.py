@@ -163,7 +163,7 @@ def test_chunked_equals_single_shot_bitwise(k_ret, chunk, dev):
     for c0 in range(0, N, chunk):
         c1 = c0 + chunk
         starts = torch.tensor([c0], dtype=torch.int32, device=dev)
-        torch.ops.atflash.kv_write(cache.k, cache.v, k[:, c0:c1], v[:, c0:c1], starts, table, rt, 0)
+        torch.ops.atflash.kv_write(cache.kv, k[:, c0:c1], v[:, c0:c1], starts, table, rt, 0)
         o, _ = interface.prefill_paged(q[:, c0:c1], cache, table, nk=c1, q_offset=c0, zhi=zhi, rope=rt)
         outs.append(o)
     chunked = torch.cat(outs, dim=1)

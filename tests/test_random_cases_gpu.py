@@ -98,7 +98,7 @@ def _run_decode(name, seed, case, dev):
         seqs.append((H.randn_bf16((1, n, hkv, H.D), g), H.randn_bf16((1, n, hkv, H.D), g)))
     table = cache.page_table(list(range(B)))
     for b, (k, v) in enumerate(seqs):
-        torch.ops.atflash.kv_write(cache.k, cache.v, k.to(dev), v.to(dev), torch.zeros(1, dtype=torch.int32, device=dev),
+        torch.ops.atflash.kv_write(cache.kv, k.to(dev), v.to(dev), torch.zeros(1, dtype=torch.int32, device=dev),
                                    table[b:b + 1].contiguous(), rt, 0)
     q = H.randn_bf16((B, hq, H.D), g)
     seq_lens = torch.tensor(lens, dtype=torch.int32, device=dev)

@@ -132,7 +132,7 @@ def test_every_level_count_chunked_equals_single_shot(chunk, dev):
     outs = []
     for c0 in range(0, N, chunk):
         c1 = min(N, c0 + chunk)
-        torch.ops.atflash.kv_write(cache.k, cache.v, k[:, c0:c1], v[:, c0:c1],
+        torch.ops.atflash.kv_write(cache.kv, k[:, c0:c1], v[:, c0:c1],
                                    torch.tensor([c0], dtype=torch.int32, device=dev), table, rt, 0)
         o, _ = interface.prefill_paged(q[:, c0:c1], cache, table, nk=c1, q_offset=c0, zhi=zhi, rope=rt)
         outs.append(o)

@@ -24,7 +24,7 @@ def _case(lens, hq, hkv, base, k_ret, rope, dev, seed):
     table = cache.page_table(list(range(len(lens))))
     for b, n in enumerate(lens):
         _, k, v = H.gpu_qkv(1, n, 1, hkv, dev, seed=seed + b, nq=1)
-        torch.ops.atflash.kv_write(cache.k, cache.v, k, v, torch.zeros(1, dtype=torch.int32, device=dev),
+        torch.ops.atflash.kv_write(cache.kv, k, v, torch.zeros(1, dtype=torch.int32, device=dev),
                                    table[b:b + 1].contiguous(), rt, 0)
     q = H.gpu_qkv(len(lens), 1, hq, 1, dev, seed=seed + 100, nq=1)[0][:, 0]  # [B, Hq, 128]
     zhi = None if k_ret is None else AW.window_zhi_from_kret(H.D, base, k_ret, 1 << 23)
@@ -39,7 +39,7 @@ def _decode(c, noalloc):
     out = torch.empty((B, c["hq"], H.D), dtype=torch.bfloat16, device=c["q"].device)
     rt = c["rt"]
     args = [_lib.ptr(out), out.stride(0), out.stride(1), _lib.ptr(c["q"]), c["q"].stride(0), c["q"].stride(1),
-            _lib.ptr(c["cache"].k), _lib.ptr(c["cache"].v), c["cache"].num_pages, _lib.ptr(c["table"]),
+            _lib.ptr(c["cache"].kv), c["cache"].num_pages, _lib.ptr(c["table"]),
             c["table"].shape[1], _lib.ptr(c["seq"]), B, c["hq"], c["hkv"], maxlen, _lib.zhi_array(c["zhi"]),
             H.D ** -0.5, _lib.ptr(rt), 0 if rt is None else rt.shape[0], 0]
     if noalloc:
@@ -93,7 +93,7 @@ def test_noalloc_decode_replays_in_a_hip_graph(dev):
     with torch.cuda.graph(graph):
         rc = L.atf_decode_paged_bf16_noalloc(
             _lib.ptr(out), out.stride(0), out.stride(1), _lib.ptr(c["q"]), c["q"].stride(0), c["q"].stride(1),
-            _lib.ptr(c["cache"].k), _lib.ptr(c["cache"].v), c["cache"].num_pages, _lib.ptr(c["table"]),
+            _lib.ptr(c["cache"].kv), c["cache"].num_pages, _lib.ptr(c["table"]),
             c["table"].shape[1], _lib.ptr(c["seq"]), B, 28, 4, maxlen, zhi, H.D ** -0.5, _lib.ptr(rt),
             rt.shape[0], 0, _lib.stream_of(out.device))
     _lib.check(rc)
