@@ -59,15 +59,43 @@ struct PageRegs {
   bool mask;   // per-key rule with a slice boundary inside the page
 };
 
-// Page-table entry of page p (a vector register; every lane holds the same
-// value).  The load is unconditional, its index clamped into [p_begin, p_end):
+// Page order of a split: the split's local page j (0 <= j < its page count)
+// is page po + pm * j of the sequence.  Splits of at least two 4-page groups
+// per wave interleave (po = s, pm = n_splits: split s takes pages s,
+// s + n_splits, ...), so that the workgroups of a call sweep the sequence from
+// its oldest to its youngest page together and each split holds pages of
+// every age.  Shorter splits take contiguous runs (po = s * pages_per_split,
+// pm = 1).  Measured per call against contiguous runs for every split (same
+// box, graph-replayed): with a page table in allocation order (the cache's
+// own allocators) Qwen 128K OFF -3.5%, k=2 -8.5%, Llama 32K -6 to -9%, Llama
+// 128K -2.5 to -5%; with randomly permuted pages +0.4% OFF and +1% at k=2 at
+// Qwen 128K, no change at Llama 32K/128K; at 8K (one group per wave)
+// interleaving lost up to 4-6%, hence the threshold.  po and pm are known
+// before the sequence length is; count is set once it is.
+struct PageOrder {
+  int po, pm;
+  int count;  // the split's pages for this sequence
+};
+__device__ __forceinline__ PageOrder page_order(int s, int n_splits, int pages_per_split, int stride) {
+  const bool ilv = pages_per_split >= 2 * stride;
+  return PageOrder{ilv ? s : s * pages_per_split, ilv ? n_splits : 1, 0};
+}
+__device__ __forceinline__ void set_page_count(PageOrder& o, int s, int n_splits, int pages_per_split,
+                                               int n_pages) {
+  o.count = o.pm != 1 ? (n_pages > s ? (n_pages - s + n_splits - 1) / n_splits : 0)
+                      : max(0, min(n_pages - o.po, pages_per_split));  // (n_splits 1: the same count)
+}
+
+// Page-table entry of local page j (a vector register; every lane holds the
+// same value).  The load is unconditional, its index clamped into the split:
 // an entry for a page past the split is fetched but never used (its page is
-// not loaded).  A load guarded by a branch with a default value would make the
+// not loaded), and a split without pages reads entry po, inside the table
+// row.  A load guarded by a branch with a default value would make the
 // compiler wait for every outstanding load before the register's next use.
 // A wave fetches a page's entry one stride ahead of its use, so the page loads
 // are issued without waiting for the table.
-__device__ __forceinline__ int dec_fetch_entry(const int32_t* row, int p, int p_begin, int p_end) {
-  return row[max(p_begin, min(p, p_end - 1))];
+__device__ __forceinline__ int dec_fetch_entry(const int32_t* row, const PageOrder& o, int j) {
+  return row[o.po + o.pm * max(0, min(j, o.count - 1))];
 }
 
 // The fields of the call that the first page loads need, passed as leading
@@ -78,7 +106,7 @@ struct DecHot {
   const int32_t* page_table;
   const int32_t* seq_lens;
   const uint16_t* kv_cache;
-  int max_pages, pages_per_split, max_seq_len, hkv, num_pages;
+  int max_pages, pages_per_split, max_seq_len, hkv, num_pages, n_splits;
 };
 
 // The slices page p reads and whether an older key of it reads fewer.  Page
@@ -164,8 +192,8 @@ __device__ __forceinline__ void dec_load_page(const DecHot& a, int h, int raw, b
 template <bool kPerKey, int kWaves>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void decode_kernel(const int32_t* page_table, const int32_t* seq_lens, const uint16_t* kv_cache, int max_pages,
-                   int pages_per_split, int max_seq_len, int hkv, int num_pages, DecodeArgs a) {
-  const DecHot hot{page_table, seq_lens, kv_cache, max_pages, pages_per_split, max_seq_len, hkv, num_pages};
+                   int pages_per_split, int max_seq_len, int hkv, int num_pages, int n_splits, DecodeArgs a) {
+  const DecHot hot{page_table, seq_lens, kv_cache, max_pages, pages_per_split, max_seq_len, hkv, num_pages, n_splits};
   // wave partials
   __shared__ __attribute__((aligned(16))) float sh_o[kWaves * kDecMaxGroup * kD];
   __shared__ float sh_m[kWaves * kDecMaxGroup], sh_l[kWaves * kDecMaxGroup];
@@ -174,10 +202,12 @@ void decode_kernel(const int32_t* page_table, const int32_t* seq_lens, const uin
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int g = lane & 15;
-  const int p_begin = s * hot.pages_per_split;
-  // wave w takes the groups of kDecUnroll pages that start at p_begin + kDecUnroll * (w + kWaves * i).
+  // Local page indices: wave w takes the groups of kDecUnroll local pages that
+  // start at kDecUnroll * (w + kWaves * i); local page j is page po + pm * j.
   constexpr int kStride = kDecUnroll * kWaves;
-  const int p_first = p_begin + kDecUnroll * __builtin_amdgcn_readfirstlane(wave);
+  const int p_first = kDecUnroll * __builtin_amdgcn_readfirstlane(wave);
+  PageOrder ord = page_order(s, hot.n_splits, hot.pages_per_split, kStride);
+  const int po = ord.po, pm = ord.pm;
   // The first group's page-table entries are fetched together with the
   // sequence length, their index clamped into the table row only (an entry
   // past the split is never used), so the first page loads wait for two
@@ -185,10 +215,11 @@ void decode_kernel(const int32_t* page_table, const int32_t* seq_lens, const uin
   int ent[kDecUnroll];
   const int32_t* row = hot.page_table + static_cast<int64_t>(b) * hot.max_pages;
 #pragma unroll
-  for (int u = 0; u < kDecUnroll; ++u) ent[u] = row[min(p_first + u, hot.max_pages - 1)];
+  for (int u = 0; u < kDecUnroll; ++u) ent[u] = row[min(po + pm * (p_first + u), hot.max_pages - 1)];
   const int N = max(0, min(hot.seq_lens[b], hot.max_seq_len));
   const int n_pages = (N + kPage - 1) / kPage;
-  const int p_end = min(n_pages, p_begin + hot.pages_per_split);
+  set_page_count(ord, s, hot.n_splits, hot.pages_per_split, n_pages);
+  const int p_end = ord.count;
   const float NEG_INF = -__builtin_huge_valf();
   const float c = a.scale_log2;
 
@@ -214,11 +245,11 @@ void decode_kernel(const int32_t* page_table, const int32_t* seq_lens, const uin
   for (int u = 0; u < kDecUnroll; ++u) {
     int ns;
     bool mask;
-    page_slices<kPerKey>(a, zc, p_first + u, N, ns, mask);
-    dec_load_page(hot, h, ent[u], p_first + u < p_end, p_first + u, ns, mask, lane, pr[u]);
+    page_slices<kPerKey>(a, zc, po + pm * (p_first + u), N, ns, mask);
+    dec_load_page(hot, h, ent[u], p_first + u < p_end, po + pm * (p_first + u), ns, mask, lane, pr[u]);
   }
 #pragma unroll
-  for (int u = 0; u < kDecUnroll; ++u) ent[u] = dec_fetch_entry(row, p_first + kStride + u, p_begin, p_end);
+  for (int u = 0; u < kDecUnroll; ++u) ent[u] = dec_fetch_entry(row, ord, p_first + kStride + u);
 
   // ---- Q^T fragments: lane holds q head g, slice 4 lp + lane/16 ----
   // Every Q and (cos, sin) load is issued before any is used (one memory round
@@ -288,7 +319,7 @@ void decode_kernel(const int32_t* page_table, const int32_t* seq_lens, const uin
       PageRef ref_n{0, false};
       if (reload) {
         int ns;
-        page_slices<kPerKey>(a, zc, pn, N, ns, mask_n);
+        page_slices<kPerKey>(a, zc, po + pm * pn, N, ns, mask_n);
         ref_n = page_ref(hot, h, ent[u], true);
         dec_load_k(hot, ref_n, ns, lane, r.k);
       }
@@ -338,9 +369,9 @@ void decode_kernel(const int32_t* page_table, const int32_t* seq_lens, const uin
         O[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, r.v[db]), pb, O[db], 0, 0, 0);
       if (reload) {
         dec_load_v(hot, ref_n, lane, r.v);
-        r.n0 = pn * kPage;
+        r.n0 = (po + pm * pn) * kPage;
         r.mask = mask_n;
-        ent[u] = dec_fetch_entry(row, pn + kStride, p_begin, p_end);
+        ent[u] = dec_fetch_entry(row, ord, pn + kStride);
       }
     }
   }
@@ -403,20 +434,22 @@ __global__ __launch_bounds__(kDecWaves * 64) __attribute__((amdgpu_waves_per_eu(
 void decode_stream_probe_kernel(const int32_t* page_table, const int32_t* seq_lens, const uint16_t* kv_cache,
                                 int max_pages, int pages_per_split, int max_seq_len, int hkv, int num_pages,
                                 int n_splits, uint32_t* sink, DecodeArgs a) {
-  const DecHot hot{page_table, seq_lens, kv_cache, max_pages, pages_per_split, max_seq_len, hkv, num_pages};
+  const DecHot hot{page_table, seq_lens, kv_cache, max_pages, pages_per_split, max_seq_len, hkv, num_pages, n_splits};
   const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
-  const int p_begin = s * hot.pages_per_split;
   constexpr int kStride = kDecUnroll * kDecWaves;
-  const int p_first = p_begin + kDecUnroll * __builtin_amdgcn_readfirstlane(wave);
+  const int p_first = kDecUnroll * __builtin_amdgcn_readfirstlane(wave);
+  PageOrder ord = page_order(s, hot.n_splits, hot.pages_per_split, kStride);
+  const int po = ord.po, pm = ord.pm;
   int ent[kDecUnroll];
   const int32_t* row = hot.page_table + static_cast<int64_t>(b) * hot.max_pages;
 #pragma unroll
-  for (int u = 0; u < kDecUnroll; ++u) ent[u] = row[min(p_first + u, hot.max_pages - 1)];
+  for (int u = 0; u < kDecUnroll; ++u) ent[u] = row[min(po + pm * (p_first + u), hot.max_pages - 1)];
   const int N = max(0, min(hot.seq_lens[b], hot.max_seq_len));
   const int n_pages = (N + kPage - 1) / kPage;
-  const int p_end = min(n_pages, p_begin + hot.pages_per_split);
+  set_page_count(ord, s, hot.n_splits, hot.pages_per_split, n_pages);
+  const int p_end = ord.count;
   PageRegs pr[kDecUnroll];
   int zc = INT32_MIN;
 #pragma unroll
@@ -426,11 +459,11 @@ void decode_stream_probe_kernel(const int32_t* page_table, const int32_t* seq_le
   for (int u = 0; u < kDecUnroll; ++u) {
     int ns;
     bool mask;
-    page_slices<true>(a, zc, p_first + u, N, ns, mask);
-    dec_load_page(hot, h, ent[u], p_first + u < p_end, p_first + u, ns, false, lane, pr[u]);
+    page_slices<true>(a, zc, po + pm * (p_first + u), N, ns, mask);
+    dec_load_page(hot, h, ent[u], p_first + u < p_end, po + pm * (p_first + u), ns, false, lane, pr[u]);
   }
 #pragma unroll
-  for (int u = 0; u < kDecUnroll; ++u) ent[u] = dec_fetch_entry(row, p_first + kStride + u, p_begin, p_end);
+  for (int u = 0; u < kDecUnroll; ++u) ent[u] = dec_fetch_entry(row, ord, p_first + kStride + u);
   uint32_t acc = 0;
   for (int p0 = p_first; p0 < p_end; p0 += kStride) {
 #pragma unroll
@@ -445,9 +478,9 @@ void decode_stream_probe_kernel(const int32_t* page_table, const int32_t* seq_le
       if (pn < p_end) {
         int ns;
         bool mask;
-        page_slices<true>(a, zc, pn, N, ns, mask);
-        dec_load_page(hot, h, ent[u], true, pn, ns, false, lane, pr[u]);
-        ent[u] = dec_fetch_entry(row, pn + kStride, p_begin, p_end);
+        page_slices<true>(a, zc, po + pm * pn, N, ns, mask);
+        dec_load_page(hot, h, ent[u], true, po + pm * pn, ns, false, lane, pr[u]);
+        ent[u] = dec_fetch_entry(row, ord, pn + kStride);
       }
     }
   }
@@ -643,7 +676,7 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t s) {
   const dim3 grid(a.n_splits, a.hkv, a.batch);
 #define ATF_DEC_LAUNCH(PK, W)                                                                                   \
   hipLaunchKernelGGL((decode_kernel<PK, W>), grid, dim3(W * 64), 0, s, a.page_table, a.seq_lens, a.kv_cache,    \
-                     a.max_pages, a.pages_per_split, a.max_seq_len, a.hkv, a.num_pages, a)
+                     a.max_pages, a.pages_per_split, a.max_seq_len, a.hkv, a.num_pages, a.n_splits, a)
   if (a.waves == 8) {
     if (a.per_key) ATF_DEC_LAUNCH(true, 8); else ATF_DEC_LAUNCH(false, 8);
   } else {
