@@ -60,24 +60,28 @@ struct PageRegs {
 };
 
 // Page order of a split: the split's local page j (0 <= j < its page count)
-// is page po + pm * j of the sequence.  Splits of at least two 4-page groups
-// per wave interleave (po = s, pm = n_splits: split s takes pages s,
-// s + n_splits, ...), so that the workgroups of a call sweep the sequence from
-// its oldest to its youngest page together and each split holds pages of
-// every age.  Shorter splits take contiguous runs (po = s * pages_per_split,
-// pm = 1).  Measured per call against contiguous runs for every split (same
-// box, graph-replayed): with a page table in allocation order (the cache's
-// own allocators) Qwen 128K OFF -3.5%, k=2 -8.5%, Llama 32K -6 to -9%, Llama
-// 128K -2.5 to -5%; with randomly permuted pages +0.4% OFF and +1% at k=2 at
-// Qwen 128K, no change at Llama 32K/128K; at 8K (one group per wave)
-// interleaving lost up to 4-6%, hence the threshold.  po and pm are known
-// before the sequence length is; count is set once it is.
+// is page po + pm * j of the sequence.  Splits of at least kDecIlvMinPages
+// pages (one 4-page group per wave of an 8-wave workgroup) interleave
+// (po = s, pm = n_splits: split s takes pages s, s + n_splits, ...), so that
+// the workgroups of a call sweep the sequence from its oldest to its youngest
+// page together and each split holds pages of every age.  Shorter splits (the
+// 4-wave workgroups of short contexts) take contiguous runs
+// (po = s * pages_per_split, pm = 1).  Measured per call against contiguous
+// runs for every split (same box, graph-replayed; pools rotated past the
+// last-level cache): with a page table in allocation order (the cache's own
+// allocators) Qwen 128K OFF -2 to -4%, k=2 -8 to -10% (three runs), Llama 32K
+// OFF -2.5 to -8.5%, k=2 -8.5 to -9.5%, Llama 128K OFF -2.5%, k=2 -5.5%,
+// Llama 16K OFF -6.5%, k=2 -12%, Qwen 32K -2%; with randomly permuted pages
+// +0.3 to +1.3% at those shapes; at 8K with 4-wave workgroups interleaving lost
+// up to 4-6%.  po and pm are known before the sequence length is; count is set
+// once it is.
+constexpr int kDecIlvMinPages = kDecUnroll * kDecWaves;
 struct PageOrder {
   int po, pm;
   int count;  // the split's pages for this sequence
 };
-__device__ __forceinline__ PageOrder page_order(int s, int n_splits, int pages_per_split, int stride) {
-  const bool ilv = pages_per_split >= 2 * stride;
+__device__ __forceinline__ PageOrder page_order(int s, int n_splits, int pages_per_split) {
+  const bool ilv = pages_per_split >= kDecIlvMinPages;
   return PageOrder{ilv ? s : s * pages_per_split, ilv ? n_splits : 1, 0};
 }
 __device__ __forceinline__ void set_page_count(PageOrder& o, int s, int n_splits, int pages_per_split,
@@ -206,7 +210,7 @@ void decode_kernel(const int32_t* page_table, const int32_t* seq_lens, const uin
   // start at kDecUnroll * (w + kWaves * i); local page j is page po + pm * j.
   constexpr int kStride = kDecUnroll * kWaves;
   const int p_first = kDecUnroll * __builtin_amdgcn_readfirstlane(wave);
-  PageOrder ord = page_order(s, hot.n_splits, hot.pages_per_split, kStride);
+  PageOrder ord = page_order(s, hot.n_splits, hot.pages_per_split);
   const int po = ord.po, pm = ord.pm;
   // The first group's page-table entries are fetched together with the
   // sequence length, their index clamped into the table row only (an entry
@@ -440,7 +444,7 @@ void decode_stream_probe_kernel(const int32_t* page_table, const int32_t* seq_le
   const int wave = tid >> 6, lane = tid & 63;
   constexpr int kStride = kDecUnroll * kDecWaves;
   const int p_first = kDecUnroll * __builtin_amdgcn_readfirstlane(wave);
-  PageOrder ord = page_order(s, hot.n_splits, hot.pages_per_split, kStride);
+  PageOrder ord = page_order(s, hot.n_splits, hot.pages_per_split);
   const int po = ord.po, pm = ord.pm;
   int ent[kDecUnroll];
   const int32_t* row = hot.page_table + static_cast<int64_t>(b) * hot.max_pages;

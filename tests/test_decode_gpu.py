@@ -136,6 +136,53 @@ def test_ragged_batch_with_empty_sequences(dev):
                 H.assert_close(out[b], ref, f"seq {b} len {lens[b]} window {name}")
 
 
+def test_interleaved_splits_ragged_batch(dev):
+    """Splits of at least 32 pages (one 4-page group per wave of 8) take every
+    n_splits-th page of a sequence (split s: pages s, s + n_splits, ...).  A ragged batch
+    whose longest sequence selects that order: the 33-token sequence has 3
+    pages, so all but three splits of its kv heads hold no page, and the empty
+    sequence none at all; every sequence matches the oracle (window OFF, level
+    table, vec8 table), the empty one is exactly zero."""
+    from atflash import _lib, atflash_window as AW, fiwin_common as FW, interface, rope as R
+    from atflash.cache import PagedKVCache
+    base, hq, hkv = 1e7, 8, 2
+    lens = [40000, 33, 0, 17000]
+    B, maxlen = len(lens), max(lens)
+    # the split rule gives 32 splits of 79 pages: interleaved (>= 32 pages per split)
+    ns = _lib.lib().atf_decode_workspace_bytes(B, hq, hkv, maxlen) // (B * hkv * 16 * 130 * 4)
+    pps = -(-(-(-maxlen // 16)) // ns)
+    assert ns == 32 and pps >= 32, (ns, pps)
+    cache = PagedKVCache(sum(-(-n // 16) for n in lens) + 3, hkv, dev)
+    cache._free = torch.randperm(len(cache._free), generator=torch.Generator().manual_seed(11)).tolist()
+    rt = R.rope_table(maxlen, R.inv_freq(H.D, base, dev))
+    g = torch.Generator().manual_seed(99)
+    seqs = []
+    for b, n in enumerate(lens):
+        cache.add_sequence(b, n)
+        seqs.append((H.randn_bf16((1, n, hkv, H.D), g), H.randn_bf16((1, n, hkv, H.D), g)))
+    table = cache.page_table(list(range(B)))
+    for b, (k, v) in enumerate(seqs):
+        if lens[b]:
+            torch.ops.atflash.kv_write(cache.kv, k.to(dev), v.to(dev),
+                                       torch.zeros(1, dtype=torch.int32, device=dev), table[b:b + 1].contiguous(), rt, 0)
+    q = H.randn_bf16((B, hq, H.D), g)
+    seq_lens = torch.tensor(lens, dtype=torch.int32, device=dev)
+    tables = {"off": None, "level": AW.window_zhi_from_kret(H.D, base, 2.0, 1 << 20),
+              "vec8": FW.zhi_slice_vec8(H.D, base, 2.0).tolist()}
+    for name, z in tables.items():
+        print(f"[decode parity] interleaved splits, batch {lens}, window {name}", flush=True)
+        out = interface.decode_paged(q.to(dev), cache, table, seq_lens, maxlen, zhi=z, rope=rt).cpu()
+        for b, (k, v) in enumerate(seqs):
+            if lens[b] == 0:
+                assert torch.equal(out[b], torch.zeros_like(out[b])), f"empty sequence {b}, window {name}"
+            elif name == "vec8":
+                H.assert_close(out[b], H.decode_oracle_vec8(q[b], k[0], v[0], base, list(z), rope=True),
+                               f"seq {b} len {lens[b]} window vec8")
+            else:
+                ref = H.decode_oracle(q[b], k[0], v[0], base, 2.0 if z else float("inf"), True)
+                H.assert_close(out[b], ref, f"seq {b} len {lens[b]} window {name}")
+
+
 def test_decode_off_equals_k_inf_bitwise(dev):
     from atflash import atflash_window as AW
     g = torch.Generator().manual_seed(5)
