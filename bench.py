@@ -42,9 +42,13 @@ decode    besides the eager back-to-back figure, every decode configuration is
           the host's per-call work, which sets an eager loop's pace at short
           contexts.
 detail    the other published configurations (Llama-3.2-3B prefill and decode,
-          Qwen2.5-7B chunked prefill to 512K and decode at 512K) and C5, one
-          whole request on the random-init 28-layer Qwen2.5-7B (256K prompt in
-          64K chunks, 64 greedy steps; window OFF, k = 2, k = 64).
+          Qwen2.5-7B chunked prefill to 512K and decode at 512K), the 128K
+          decode with other page arrangements (a sequence's pages scattered
+          over a 1 GiB pool shared with three others, or in allocation order;
+          the headline decode permutes them inside the sequence's own pool)
+          and C5, one whole request on the random-init 28-layer Qwen2.5-7B
+          (256K prompt in 64K chunks, 64 greedy steps; window OFF, k = 2,
+          k = 64).
 """
 import argparse
 import json
@@ -524,6 +528,52 @@ def bench_detail(steps=3):
               f"({r['on_over_off']:.3f}x; reference {r['reference_ratio']:.3f}x)", flush=True)
         del q, kvc, table, rt
         torch.cuda.empty_cache()
+
+    # ---- Qwen2.5-7B decode at 128K by page arrangement: the headline decode
+    # permutes each sequence's pages inside its own 268 MB pool; here four
+    # sequences share one 1 GiB pool, each call reading one of them, with its
+    # pages scattered over the whole pool or in allocation order ----
+    N = 131072
+    pages = N // 16
+    copies = 4
+    rt = R.rope_table(N, R.inv_freq(D, BASE, dev))
+    pool = PagedKVCache(copies * pages, HKV, dev)
+    g = torch.Generator(device=dev).manual_seed(6)
+    k = torch.randn((1, N, HKV, D), generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn((1, N, HKV, D), generator=g, device=dev).to(torch.bfloat16)
+    q = torch.randn((1, HQ, D), generator=g, device=dev).to(torch.bfloat16)
+    seq = torch.tensor([N], dtype=torch.int32, device=dev)
+    perm = torch.randperm(copies * pages, generator=torch.Generator().manual_seed(6)).to(torch.int32)
+    arrangements = {
+        "scattered_1GiB": [perm[c * pages:(c + 1) * pages].view(1, -1).to(dev) for c in range(copies)],
+        "allocation_order": [torch.arange(c * pages, (c + 1) * pages, dtype=torch.int32).view(1, -1).to(dev)
+                             for c in range(copies)]}
+    out["qwen_decode_page_order"] = {}
+    for arr, tables in arrangements.items():
+        for tab in tables:
+            torch.ops.atflash.kv_write(pool.kv, k, v, torch.zeros(1, dtype=torch.int32, device=dev), tab, rt, 0)
+        r = {}
+        for name, zhi in (("off", None), ("k2", list(AW.window_zhi_from_kret(D, BASE, 2.0, 1 << 23))),
+                          ("k2_vec8", FW.zhi_slice_vec8(D, BASE, 2.0).tolist())):
+            it = [0]
+
+            def fn():
+                t = tables[it[0] % copies]
+                it[0] += 1
+                return ops.decode_paged(q, pool.kv, t, seq, N, zhi, D ** -0.5, rt, 0)
+            for _ in range(10):
+                fn()
+            r[name + "_us"] = _events_time_median(fn, 40 * steps) * 1e3
+            r[name + "_graph_us"] = _graph_time(fn, 8 * copies) * 1e3
+        r["on_over_off"] = r["off_us"] / r["k2_us"]
+        r["on_over_off_vec8"] = r["off_us"] / r["k2_vec8_us"]
+        r["off_frac_of_8TBs"] = N * HKV * D * 2 * 2 / (r["off_us"] * 1e-6) / PEAK_HBM
+        out["qwen_decode_page_order"][arr] = r
+        print(f"[bench detail] qwen decode 128K, pages {arr}: off {r['off_us']:.2f} us, k2 {r['k2_us']:.2f} us "
+              f"({r['on_over_off']:.3f}x), k2 vec8 {r['k2_vec8_us']:.2f} us ({r['on_over_off_vec8']:.3f}x); "
+              f"OFF {r['off_frac_of_8TBs']:.3f} of 8 TB/s", flush=True)
+    del pool, arrangements, k, v, q, rt, perm
+    torch.cuda.empty_cache()
 
     # ---- Qwen2.5-7B decode at 512K (batch 1, permuted pages, one 2 GB pool) ----
     N = 524288
