@@ -136,7 +136,7 @@ size_t atf_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, 
  * aligned, strides multiples of 8; out: 8-byte aligned, strides multiples of 4); seq_lens is a
  * device int32 [batch] whose entries must not exceed max_seq_len.  The window
  * is quantized per page (block_n = 16): page p reads its first L(p) levels only
- * (2 L(p) slices of its K block).
+ * (2 L(p) slices of its K half).
  *
  * Replaces flashinfer.decode.single_decode_with_kv_cache_with_jit_module(...,
  * maybe_zhi_slice=...) of the FlashInfer window port
