@@ -316,7 +316,7 @@ class WindowAttention:
             if (owner.rope_cs is not None) != self.rope_at_load:
                 raise ValueError("the cache was made for the other RoPE mode of this hook")
             if L == 1:
-                zhi = list(self.window.decode_zhi8) if windowed else None
+                zhi = self.window.decode_zhi8 if windowed else None
                 o = ops.decode_paged(query[:, :, 0, :], lyr.kv, owner.page_table, owner.seq_lens(S), S, zhi,
                                      scale, owner.rope_cs, _lib.LAYOUT_HALF_SPLIT)
                 return o.view(b, 1, hq, d), None
@@ -335,7 +335,7 @@ class WindowAttention:
         if L == 1:
             kvc, table = I.pack_kv(key.transpose(1, 2), value.transpose(1, 2), rope=rt)
             seq = torch.full((b,), S, dtype=torch.int32, device=query.device)
-            zhi = list(self.window.decode_zhi8) if windowed else None
+            zhi = self.window.decode_zhi8 if windowed else None
             o = ops.decode_paged(query[:, :, 0, :], kvc, table, seq, S, zhi, scale, rt, 0)
             return o.view(b, 1, hq, d), None
         zhi = self.window.prefill_zhi if windowed else None

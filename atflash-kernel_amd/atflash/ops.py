@@ -149,6 +149,27 @@ def _decode_workspace(device, handle, B, hq, hkv, max_seq_len, L):
     return ws
 
 
+# Window tables passed as tuples, by identity: id -> (the tuple, its int32
+# array).  A tuple cannot change and the memo keeps it alive (so its id is not
+# reused), so a call that passes the same tuple again takes its array without
+# hashing the values (about 0.6 us of a short decode's host time; the HF hook's
+# tables are tuples).  Lists go through the value-keyed cache of _lib.
+_TABLE_MEMO = {}
+
+
+def _table(zhi, n):
+    if type(zhi) is not tuple:
+        return _lib.zhi_array(zhi, n)
+    hit = _TABLE_MEMO.get(id(zhi))
+    if hit is not None and hit[0] is zhi:
+        return hit[1]
+    arr = _lib.zhi_array(zhi, n)
+    if len(_TABLE_MEMO) >= 64:
+        _TABLE_MEMO.clear()
+    _TABLE_MEMO[id(zhi)] = (zhi, arr)
+    return arr
+
+
 def decode_paged(q: torch.Tensor, kv_cache: torch.Tensor, page_table: torch.Tensor,
                  seq_lens: torch.Tensor, max_seq_len: int, zhi: Optional[List[int]], sm_scale: float,
                  rope_cs: Optional[torch.Tensor], layout: int) -> torch.Tensor:
@@ -175,7 +196,7 @@ def decode_paged(q: torch.Tensor, kv_cache: torch.Tensor, page_table: torch.Tens
     out = torch.empty((B, Hq, _lib.HEAD_DIM), dtype=torch.bfloat16, device=dev)
     slices = zhi is not None and len(zhi) == _lib.SLICES
     entry = L.atf_decode_paged_slices_bf16 if slices else L.atf_decode_paged_bf16
-    table = _lib.zhi_array(zhi, _lib.SLICES if slices else _lib.LEVELS)
+    table = _table(zhi, _lib.SLICES if slices else _lib.LEVELS)
     if not seq_lens.is_contiguous():
         seq_lens = seq_lens.contiguous()
     _lib.check(entry(

@@ -349,7 +349,7 @@ def bench_gpu(args):
     for name, k_ret in (("k2_vec8", 2.0), ("k64_vec8", 64.0)):
         dec_windows[name] = FW.zhi_slice_vec8(D, BASE, k_ret).tolist()
     for name, zhi in (dec_windows.items() if args.only in ("all", "decode") else []):
-        zl = None if zhi is None else list(zhi)
+        zl = None if zhi is None else tuple(zhi)  # a tuple: the op takes its table by identity
         it = [0]
 
         def fn():
@@ -480,7 +480,7 @@ def bench_detail(steps=3):
             q = torch.randn((B, hq, D), generator=g, device=dev).to(torch.bfloat16)
             seq = torch.full((B,), N, dtype=torch.int32, device=dev)
             r = {"kv_pool_bytes": copies * B * pages * hkv * 8192}
-            for name, zhi in (("off", None), ("k2", list(AW.window_zhi_from_kret(D, base, 2.0, 1 << 23)))):
+            for name, zhi in (("off", None), ("k2", tuple(AW.window_zhi_from_kret(D, base, 2.0, 1 << 23)))):
                 it = [0]
 
                 def fn():
@@ -553,8 +553,8 @@ def bench_detail(steps=3):
         for tab in tables:
             torch.ops.atflash.kv_write(pool.kv, k, v, torch.zeros(1, dtype=torch.int32, device=dev), tab, rt, 0)
         r = {}
-        for name, zhi in (("off", None), ("k2", list(AW.window_zhi_from_kret(D, BASE, 2.0, 1 << 23))),
-                          ("k2_vec8", FW.zhi_slice_vec8(D, BASE, 2.0).tolist())):
+        for name, zhi in (("off", None), ("k2", tuple(AW.window_zhi_from_kret(D, BASE, 2.0, 1 << 23))),
+                          ("k2_vec8", tuple(FW.zhi_slice_vec8(D, BASE, 2.0).tolist()))):
             it = [0]
 
             def fn():
@@ -591,8 +591,8 @@ def bench_detail(steps=3):
     q = torch.randn((1, HQ, D), generator=g, device=dev).to(torch.bfloat16)
     seq = torch.tensor([N], dtype=torch.int32, device=dev)
     r = {"kv_pool_bytes": pages * HKV * 8192}
-    for name, zhi in (("off", None), ("k2", list(AW.window_zhi_from_kret(D, BASE, 2.0, 1 << 23))),
-                      ("k2_vec8", FW.zhi_slice_vec8(D, BASE, 2.0).tolist())):
+    for name, zhi in (("off", None), ("k2", tuple(AW.window_zhi_from_kret(D, BASE, 2.0, 1 << 23))),
+                      ("k2_vec8", tuple(FW.zhi_slice_vec8(D, BASE, 2.0).tolist()))):
         fn = lambda: ops.decode_paged(q, pool.kv, tab, seq, N, zhi, D ** -0.5, rt, 0)  # noqa: E731
         for _ in range(10):
             fn()

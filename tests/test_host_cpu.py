@@ -339,3 +339,14 @@ def test_registered_ops_and_direct_functions_agree():
     # the window table arrays are built once per table and reused
     assert _lib.zhi_array([7] * 16, _lib.SLICES) is _lib.zhi_array(tuple([7] * 16), _lib.SLICES)
     assert list(_lib.zhi_array([9] * 8)) == [9] * 8
+    # the decode takes a tuple's table by identity (a tuple cannot change), a
+    # list's by value; an equal tuple and a changed list both give the values
+    t = (9, 8, 7, 6, 5, 4, 3, 2)
+    assert ops._table(t, 8) is ops._table(t, 8)
+    assert list(ops._table(t, 8)) == list(t)
+    assert list(ops._table(tuple(t), 8)) == list(t)
+    lst = list(t)
+    first = list(ops._table(lst, 8))
+    lst[7] = 1
+    assert first == list(t) and list(ops._table(lst, 8)) == [9, 8, 7, 6, 5, 4, 3, 1]
+    assert ops._table(None, 8) is None
