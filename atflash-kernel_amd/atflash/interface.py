@@ -8,7 +8,8 @@ prefill  `_flash_attn_fwd(q, k, v, causal=True, pack_gqa=..., atflash_window_zhi
 decode   `single_decode_with_kv_cache(q, k, v, maybe_zhi=...)` as the FlashInfer
          port's single-request decode (kernels/flashinfer_port/fiwin_common.py:96-112):
          q [Hq, 128], k/v NHD [N, Hkv, 128] or HND [Hkv, N, 128].
-paged    `prefill_paged` / `decode_paged` on a PagedKVCache, the serving path.
+paged    `prefill_paged` / `decode_paged` on a PagedKVCache, the serving path;
+         `decode_plan` prepares a decode step once for a loop that repeats it.
 
 Cost of the contiguous entry points: `_flash_attn_fwd` and
 `single_decode_with_kv_cache` take the whole history as contiguous k/v, like the
@@ -122,3 +123,13 @@ def decode_paged(q, cache, page_table, seq_lens, max_seq_len, zhi=None, sm_scale
     scale = 1.0 / math.sqrt(q.shape[-1]) if sm_scale is None else float(sm_scale)
     return ops.decode_paged(q, cache.kv, page_table, seq_lens, int(max_seq_len),
                             _zhi_list(zhi, _DECODE_TABLES), scale, rope, _layout_id(layout))
+
+
+def decode_plan(cache, page_table, seq_lens, max_seq_len, num_q_heads, zhi=None, sm_scale=None, rope=None,
+                layout="half_split", q_strides=None):
+    """ops.DecodePlan for a PagedKVCache: the decode step of a serving loop
+    prepared once (cache, page table, sequence lengths updated in place,
+    window table, scale, RoPE table); plan.run(q) per step."""
+    scale = 1.0 / math.sqrt(_lib.HEAD_DIM) if sm_scale is None else float(sm_scale)
+    return ops.DecodePlan(cache.kv, page_table, seq_lens, int(max_seq_len), _zhi_list(zhi, _DECODE_TABLES), scale,
+                          rope, _layout_id(layout), num_q_heads, q_strides)

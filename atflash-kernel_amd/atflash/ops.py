@@ -207,6 +207,63 @@ def decode_paged(q: torch.Tensor, kv_cache: torch.Tensor, page_table: torch.Tens
     return out
 
 
+class DecodePlan:
+    """A decode call prepared once and run many times (a serving loop's step).
+
+    Everything but the query is fixed and validated here: the cache, page
+    table and sequence lengths (device tensors the caller may update in place
+    between runs, e.g. after appending a token), max_seq_len, the window table,
+    sm_scale, the RoPE table, the layout and the query's shape and strides.
+    run(q) checks q against the plan and launches with the prepared arguments:
+    a few microseconds of host work instead of the checks and conversions of
+    decode_paged (at short contexts the host, not the GPU, otherwise sets the
+    pace of an eager loop).  The plan owns its workspace, so runs of one plan
+    must be ordered (one stream at a time); out= takes a preallocated output.
+    The library checks every run's arguments as it checks decode_paged's (in C,
+    so cheaply).  Same kernels and results as decode_paged.
+    """
+
+    def __init__(self, kv_cache, page_table, seq_lens, max_seq_len, zhi, sm_scale, rope_cs, layout,
+                 num_q_heads, q_strides=None):
+        _need_gpu(kv_cache, page_table, seq_lens, rope_cs)
+        _check_cache(kv_cache)
+        B = page_table.shape[0] if page_table.dim() == 2 else -1
+        _need(seq_lens.dtype == torch.int32 and seq_lens.numel() == B and seq_lens.is_contiguous(),
+              "seq_lens must be contiguous int32 [B]")
+        _need(page_table.dtype == torch.int32 and page_table.dim() == 2 and page_table.is_contiguous(),
+              "page_table must be contiguous int32 [B, max_pages]")
+        Hq = int(num_q_heads)
+        D = _lib.HEAD_DIM
+        q_sb, q_sh = q_strides if q_strides is not None else (Hq * D, D)
+        rope_cs, max_pos = _rope(rope_cs)
+        slices = zhi is not None and len(zhi) == _lib.SLICES
+        L = _lib.lib()
+        self.device = kv_cache.device
+        self.shape = (B, Hq, D)
+        self.q_strides = (q_sb, q_sh, 1)
+        nbytes = int(L.atf_decode_workspace_bytes(B, Hq, kv_cache.shape[1], int(max_seq_len)))
+        self._ws = torch.empty((max(nbytes, 16) + 3) // 4, dtype=torch.float32, device=self.device)
+        self._keep = (kv_cache, page_table, seq_lens, rope_cs)  # the tensors the addresses point into
+        self._table = _lib.zhi_array(None if zhi is None else tuple(zhi), _lib.SLICES if slices else _lib.LEVELS)
+        self._entry = L.atf_decode_paged_slices_bf16 if slices else L.atf_decode_paged_bf16
+        self._mid = (kv_cache.data_ptr(), kv_cache.shape[0], page_table.data_ptr(), page_table.shape[1],
+                     seq_lens.data_ptr(), B, Hq, kv_cache.shape[1], int(max_seq_len), self._table, float(sm_scale),
+                     _lib.ptr(rope_cs), max_pos, _layout(layout), self._ws.data_ptr(), self._ws.numel() * 4)
+
+    def run(self, q: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Decode for q [B, Hq, 128] bf16 (the plan's shape and strides);
+        returns out (allocated unless given: bf16 [B, Hq, 128], contiguous)."""
+        if q.shape != self.shape or q.stride() != self.q_strides or q.dtype != torch.bfloat16 or not q.is_cuda:
+            raise ValueError(f"q must be bf16 {self.shape} with strides {self.q_strides} on the plan's device")
+        if out is None:
+            out = torch.empty(self.shape, dtype=torch.bfloat16, device=self.device)
+        elif out.shape != self.shape or not out.is_contiguous() or out.dtype != torch.bfloat16:
+            raise ValueError(f"out must be contiguous bf16 {self.shape}")
+        _lib.check(self._entry(out.data_ptr(), self.shape[1] * _lib.HEAD_DIM, _lib.HEAD_DIM, q.data_ptr(),
+                               self.q_strides[0], self.q_strides[1], *self._mid, _lib.stream_of(self.device)))
+        return out
+
+
 _decode_paged_op = torch.library.custom_op("atflash::decode_paged", decode_paged, mutates_args=())
 
 

@@ -40,7 +40,8 @@ clocks    every timed section runs with a background thread reading the GPU's
 decode    besides the eager back-to-back figure, every decode configuration is
           also replayed from a HIP graph (`*_graph_us`): the GPU time without
           the host's per-call work, which sets an eager loop's pace at short
-          contexts.
+          contexts; the Llama decode configurations are also timed through
+          prepared plans (`*_plan_us`, ops.DecodePlan, a serving loop's form).
 detail    the other published configurations (Llama-3.2-3B prefill and decode,
           Qwen2.5-7B chunked prefill to 512K and decode at 512K), the 128K
           decode with other page arrangements (a sequence's pages scattered
@@ -491,16 +492,29 @@ def bench_detail(steps=3):
                     fn()
                 r[name + "_us"] = _events_time_median(fn, 40 * steps) * 1e3
                 r[name + "_graph_us"] = _graph_time(fn, 8 * copies) * 1e3
+                # the same calls through a prepared plan per pool copy (ops.DecodePlan: the
+                # serving loop's form, a few microseconds of host work per call)
+                plans = [ops.DecodePlan(pool.kv, t, seq, N, zhi, D ** -0.5, rt, 0, hq) for t in tables]
+
+                def fp():
+                    p = plans[it[0] % copies]
+                    it[0] += 1
+                    return p.run(q)
+                for _ in range(10):
+                    fp()
+                r[name + "_plan_us"] = _events_time_median(fp, 40 * steps) * 1e3
             r["on_over_off"] = r["off_us"] / r["k2_us"]
             r["on_over_off_graph"] = r["off_graph_us"] / r["k2_graph_us"]
+            r["on_over_off_plan"] = r["off_plan_us"] / r["k2_plan_us"]
             if B == 1:
                 r.update(_ref_ratio("llama_decode_b1_us", N))
             out["llama_decode"][f"b{B}_{N}"] = r
             print(f"[bench detail] llama decode B={B} {N}: off {r['off_us']:.1f} us k2 {r['k2_us']:.1f} us "
-                  f"({r['on_over_off']:.3f}x; graph replay off {r['off_graph_us']:.1f} k2 {r['k2_graph_us']:.1f} us, "
+                  f"({r['on_over_off']:.3f}x; planned off {r['off_plan_us']:.1f} k2 {r['k2_plan_us']:.1f} us, "
+                  f"{r['on_over_off_plan']:.3f}x; graph replay off {r['off_graph_us']:.1f} k2 {r['k2_graph_us']:.1f} us, "
                   f"{r['on_over_off_graph']:.3f}x" + (f"; reference {r['reference_ratio']:.3f}x)" if B == 1 else ")"),
                   flush=True)
-            del pool, tables, q, rt
+            del pool, tables, q, rt, plans
             torch.cuda.empty_cache()
 
     # ---- Qwen2.5-7B prefill of 32K, 262K and 512K tokens in 8K query chunks ----

@@ -183,6 +183,54 @@ def test_interleaved_splits_ragged_batch(dev):
                 H.assert_close(out[b], ref, f"seq {b} len {lens[b]} window {name}")
 
 
+def test_decode_plan_equals_decode_paged(dev):
+    """interface.decode_plan / ops.DecodePlan: the step of a decode loop
+    prepared once.  run(q) gives the bits of decode_paged for window OFF, the
+    level table and the vec8 table, into a fresh or a given output; after one
+    token per sequence is appended and seq_lens is updated in place, the same
+    plan gives the bits of decode_paged at the new lengths; a query of another
+    shape is refused."""
+    from atflash import atflash_window as AW, fiwin_common as FW, interface, rope as R
+    from atflash.cache import PagedKVCache
+    base, hq, hkv = 5e5, 24, 8
+    lens = [5000, 300]
+    cap = 5100
+    B = len(lens)
+    cache = PagedKVCache(B * (-(-cap // 16)) + 3, hkv, dev)
+    cache._free = torch.randperm(len(cache._free), generator=torch.Generator().manual_seed(12)).tolist()
+    rt = R.rope_table(cap, R.inv_freq(H.D, base, dev))
+    g = torch.Generator().manual_seed(13)
+    for b, n in enumerate(lens):
+        cache.add_sequence(b, cap)
+    table = cache.page_table(list(range(B)))
+    for b, n in enumerate(lens):
+        torch.ops.atflash.kv_write(cache.kv, H.randn_bf16((1, n, hkv, H.D), g).to(dev),
+                                   H.randn_bf16((1, n, hkv, H.D), g).to(dev),
+                                   torch.zeros(1, dtype=torch.int32, device=dev), table[b:b + 1].contiguous(), rt, 0)
+    seq_lens = torch.tensor(lens, dtype=torch.int32, device=dev)
+    q = H.randn_bf16((B, hq, H.D), g).to(dev)
+    tables = {"off": None, "level": AW.window_zhi_from_kret(H.D, base, 2.0, 1 << 20),
+              "vec8": FW.zhi_slice_vec8(H.D, base, 2.0).tolist()}
+    plans = {name: interface.decode_plan(cache, table, seq_lens, cap, hq, zhi=z, rope=rt) for name, z in tables.items()}
+    for name, z in tables.items():
+        print(f"[decode plan] window {name}", flush=True)
+        ref = interface.decode_paged(q, cache, table, seq_lens, cap, zhi=z, rope=rt)
+        assert torch.equal(plans[name].run(q), ref), name
+        buf = torch.empty_like(ref)
+        assert plans[name].run(q, out=buf) is buf and torch.equal(buf, ref), name
+    # one more token per sequence, written at its position; seq_lens updated in place
+    torch.ops.atflash.kv_write(cache.kv, H.randn_bf16((B, 1, hkv, H.D), g).to(dev),
+                               H.randn_bf16((B, 1, hkv, H.D), g).to(dev), seq_lens.clone(), table, rt, 0)
+    seq_lens.add_(1)
+    q2 = H.randn_bf16((B, hq, H.D), g).to(dev)
+    for name, z in tables.items():
+        print(f"[decode plan] window {name} after an append", flush=True)
+        ref = interface.decode_paged(q2, cache, table, seq_lens, cap, zhi=z, rope=rt)
+        assert torch.equal(plans[name].run(q2), ref), name
+    with pytest.raises(ValueError):
+        plans["off"].run(q2[:1])
+
+
 def test_decode_off_equals_k_inf_bitwise(dev):
     from atflash import atflash_window as AW
     g = torch.Generator().manual_seed(5)

@@ -336,6 +336,9 @@ def test_registered_ops_and_direct_functions_agree():
     for fn in (ops.kv_write, torch.ops.atflash.kv_write):
         with pytest.raises(ValueError, match="GPU"):
             fn(kvc, kv, kv, torch.zeros(1, dtype=torch.int32), table, None, 0)
+    for fn in (ops.DecodePlan,):
+        with pytest.raises(ValueError, match="GPU"):
+            fn(kvc, table, seq, 20, None, 0.1, None, 0, 4)
     # the window table arrays are built once per table and reused
     assert _lib.zhi_array([7] * 16, _lib.SLICES) is _lib.zhi_array(tuple([7] * 16), _lib.SLICES)
     assert list(_lib.zhi_array([9] * 8)) == [9] * 8
