@@ -130,6 +130,15 @@ def test_c4_qwen_decode_512k(k_ret, vec8, dev):
     _paged_decode([524288], 28, 4, 1e7, k_ret, dev, seed=45, vec8=vec8)
 
 
+@pytest.mark.parametrize("k_ret,vec8", [(2.0, True), (None, False)])
+def test_c4_qwen_decode_1m(k_ret, vec8, dev):
+    """The longest context the reference runs (its 1M end-to-end request):
+    65536 pages of one sequence, cache offsets past 2 GiB of the pool, the
+    interleaved split order, with the hook's vec8 rule at k = 2 and window OFF."""
+    print(f"[C4] qwen decode 1M k={k_ret} vec8={vec8}", flush=True)
+    _paged_decode([1048576], 28, 4, 1e7, k_ret, dev, seed=47, vec8=vec8)
+
+
 def _gpu_qkv(N, hq, hkv, dev, seed):
     g = torch.Generator(device=dev).manual_seed(seed)
     return tuple(torch.randn((1, N, h, H.D), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
