@@ -77,6 +77,30 @@ def test_qwen_128k_single_shot_window_trims_sampled_tiles(dev):
             print(f"  rows {r}: max {mx:.3e} mean {mean:.3e}", flush=True)
 
 
+def test_qwen_1m_single_shot_k2_sampled_tiles(dev):
+    """The longest context the reference runs, 1M tokens single shot at the
+    Qwen2.5-7B shape with k = 2 (RoPE fused), on sampled 32-row tiles: past a
+    distance of 231,651 only three levels are read."""
+    base, N, hq, hkv = 1e7, 1 << 20, 28, 4
+    rows = [0, 400000 // 32 * 32, 800000 // 32 * 32, N - 32]
+    q, k, v = H.gpu_qkv(1, N, hq, hkv, dev, seed=1024)
+    q_rows = {r: q[:, r:r + 32].cpu() for r in rows}
+    kc, vc = k.cpu(), v.cpu()
+    zhi = _tables(base, 2.0)
+    lv = _levels_at_rows(zhi, rows, N // 32)
+    assert int(lv[N - 32].min()) == 3 and int(lv[N - 32].max()) == 8
+    print("[qwen 1M] k2: kernel", flush=True)
+    out = _prefill(q, k, v, base, zhi, dev)
+    got = {r: out[:, r:r + 32].float().cpu() for r in rows}
+    del out, q, k, v
+    torch.cuda.empty_cache()
+    print(f"[qwen 1M] k2: oracle on {len(rows)} tiles", flush=True)
+    ref = H.prefill_oracle_rows(q_rows, kc, vc, base, 2.0, rows)
+    for r in rows:
+        mx, mean = H.assert_close(got[r], ref[r], f"k2 rows {r}")
+        print(f"  rows {r}: max {mx:.3e} mean {mean:.3e}", flush=True)
+
+
 def test_qwen_k64_8k_every_tile(dev):
     base, N, hq, hkv = 1e7, 8192, 28, 4
     zhi = _tables(base, 64.0)
