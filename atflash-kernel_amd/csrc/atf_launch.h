@@ -47,6 +47,7 @@ struct PrefillArgs {
   float* lse;  // [B][Hq][nq] natural-log LSE, or null
   const uint16_t* kv_cache;  // [num_pages][hkv][V half | K half]
   int num_pages;
+  int xcd_alt;  // serpentine XCD order (set by launch_prefill; fills the padding before page_table)
   const int32_t* page_table;
   int max_pages;
   int batch, nq, nk, q_offset, hq, hkv, group;
@@ -87,6 +88,7 @@ struct DecodeArgs {
 };
 
 hipError_t launch_kv_write(const KvWriteArgs& a, hipStream_t s);
+int prefill_xcd_alternate(int n_qtiles, int nq, int nk, int q_offset);
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t s);
 // The MFMA-ceiling probe of the prefill (measurement only): sink holds
 // ceil(ceil(nq / 256) / 8) * 8 * hq * 512 floats.

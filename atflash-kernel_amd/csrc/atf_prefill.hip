@@ -435,7 +435,11 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
   // XCD-aware block mapping: block i runs on XCD i % 8.  Each XCD walks the q
   // heads of one q-tile in order (so the heads sharing a kv head share its K/V
   // tiles in that XCD's L2), and the 8 XCDs take 8 neighbouring q-tiles, the
-  // heaviest (last) tiles first.
+  // heaviest (last) tiles first.  With a.xcd_alt the XCD order alternates from
+  // one round of 8 tiles to the next (serpentine), so that every XCD gets the
+  // same causal work over two rounds; with the same order in every round the
+  // first XCD takes the heaviest tile of every round (prefill_xcd_alternate
+  // decides per launch).
   const int bid = blockIdx.x;
   const int xcd = bid & 7;
   const int j = bid >> 3;
@@ -443,7 +447,8 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
   const int b = j / per_b;
   const int jr = j - b * per_b;
   const int h = jr % a.hq;
-  const int qrank = (jr / a.hq) * 8 + xcd;
+  const int rnd = jr / a.hq;
+  const int qrank = rnd * 8 + ((rnd & a.xcd_alt & 1) ? 7 - xcd : xcd);
   const int qt = a.n_qtiles - 1 - qrank;
   if (qt < 0 || b >= a.batch) return;
   const int kvh = h / a.group;
@@ -792,7 +797,7 @@ __device__ __forceinline__ u32x4 probe_vec(uint32_t seed, bool unit) {
 // structure at the clock the part's power limit allows.  The accumulators are
 // kept live by an empty asm statement and one store per lane at the end.
 __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_mfma_probe_kernel(int nq, int hq, int n_qtiles,
-                                                                               float* sink) {
+                                                                               int xcd_alt, float* sink) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
   lds_u8* smem = (lds_u8*)(smem_raw);
   const int tid = threadIdx.x;
@@ -802,7 +807,8 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_mfma_probe_kernel(in
   const int xcd = bid & 7;
   const int j = bid >> 3;
   const int h = j % hq;
-  const int qrank = (j / hq) * 8 + xcd;
+  const int rnd = j / hq;
+  const int qrank = rnd * 8 + ((rnd & xcd_alt & 1) ? 7 - xcd : xcd);  // prefill_kernel's order
   const int qt = n_qtiles - 1 - qrank;
   if (qt < 0) return;
   const int last_wg = min(nq, qt * kPfRowsWg + kPfRowsWg) - 1;
@@ -894,14 +900,42 @@ hipError_t ensure_lds_attribute() {
 }
 }  // namespace
 
+// Whether a launch takes the serpentine XCD order.  With the same order in
+// every round of 8 q-tiles, XCD x gets tiles n-1-x, n-9-x, ...: the first XCD
+// holds the heaviest tile of every round and finishes last.  Where that puts
+// the busiest XCD's causal work (the k-tiles of its workgroups) more than 1%
+// above the mean, the order alternates (same-box A/B, outputs bitwise equal:
+// Llama-3.2-3B shape single shot, 8K -9 to -11%, 32K -2 to -3.6%; Qwen2.5-7B
+// shape 32K in 8K chunks -1 to -1.5%; 128K single shot within noise).  Where
+// the tiles' work is nearly equal (a late chunk of a chunked prefill, whose
+// keys are mostly the cached prefix) the plain order is kept: there the
+// serpentine one measured 0 to 1% slower (Qwen2.5-7B shape, 256K in 8K chunks).
+int prefill_xcd_alternate(int n_qtiles, int nq, int nk, int q_offset) {
+  const int n_ktiles = (nk + kPfTileN - 1) / kPfTileN;
+  double tot[8] = {};
+  for (int qrank = 0; qrank < n_qtiles; ++qrank) {
+    const int qt = n_qtiles - 1 - qrank;
+    const int last = q_offset + std::min(nq, (qt + 1) * kPfRowsWg) - 1;
+    tot[qrank & 7] += std::min(n_ktiles, last / kPfTileN + 1);
+  }
+  double mx = 0.0, sum = 0.0;
+  for (double t : tot) {
+    mx = std::max(mx, t);
+    sum += t;
+  }
+  return (sum > 0.0 && 8.0 * mx > 1.01 * sum) ? 1 : 0;
+}
+
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t s) {
   if (a.nq <= 0 || a.batch <= 0) return hipSuccess;
   if (hipError_t e = ensure_lds_attribute(); e != hipSuccess) return e;
   const int blocks = a.batch * a.n_qgroups * a.hq * 8;
+  PrefillArgs k = a;
+  k.xcd_alt = prefill_xcd_alternate(a.n_qtiles, a.nq, a.nk, a.q_offset);
   if (a.rope_cs != nullptr)
-    hipLaunchKernelGGL(prefill_kernel<false>, dim3(blocks), dim3(kPfWaves * 64), kPfLdsTotal, s, a);
+    hipLaunchKernelGGL(prefill_kernel<false>, dim3(blocks), dim3(kPfWaves * 64), kPfLdsTotal, s, k);
   else
-    hipLaunchKernelGGL(prefill_kernel<true>, dim3(blocks), dim3(kPfWaves * 64), kPfLdsTotal, s, a);
+    hipLaunchKernelGGL(prefill_kernel<true>, dim3(blocks), dim3(kPfWaves * 64), kPfLdsTotal, s, k);
   return hipGetLastError();
 }
 
@@ -911,7 +945,7 @@ hipError_t launch_prefill_mfma_probe(float* sink, int nq, int hq, hipStream_t s)
   const int n_qtiles = (nq + kPfRowsWg - 1) / kPfRowsWg;
   const int blocks = ((n_qtiles + 7) / 8) * hq * 8;
   hipLaunchKernelGGL(prefill_mfma_probe_kernel, dim3(blocks), dim3(kPfWaves * 64), kPfLdsTotal, s, nq, hq, n_qtiles,
-                     sink);
+                     prefill_xcd_alternate(n_qtiles, nq, nq, 0), sink);
   return hipGetLastError();
 }
 
