@@ -27,7 +27,7 @@ from . import _lib
 
 def _need_gpu(*ts):
     for t in ts:
-        if t is not None and t.device.type != "cuda":
+        if t is not None and not t.is_cuda:
             raise ValueError("atflash ops run on the GPU only (got a tensor on %s)" % t.device)
 
 
@@ -37,6 +37,10 @@ def _need(cond, msg):
 
 
 def _check_cache(kv_cache):
+    s = kv_cache.shape
+    if (kv_cache.dtype == torch.bfloat16 and len(s) == 4 and s[2] == _lib.KV_BLOCK_SHAPE[0]
+            and s[3] == _lib.KV_BLOCK_SHAPE[1] and kv_cache.is_contiguous()):
+        return  # the common case in one test (this runs on every call)
     _need(kv_cache.dtype == torch.bfloat16, "kv_cache must be bf16")
     _need(kv_cache.dim() == 4 and tuple(kv_cache.shape[2:]) == _lib.KV_BLOCK_SHAPE,
           "kv_cache must be [num_pages, num_kv_heads, 2, 2048]")
@@ -51,9 +55,10 @@ def _layout(layout: int) -> int:
 def _rope(rope_cs):
     if rope_cs is None:
         return None, 0
-    _need(rope_cs.dtype == torch.float32 and rope_cs.dim() == 3 and rope_cs.shape[1:] == (_lib.HEAD_DIM // 2, 2)
+    s = rope_cs.shape
+    _need(rope_cs.dtype == torch.float32 and len(s) == 3 and s[1] == _lib.HEAD_DIM // 2 and s[2] == 2
           and rope_cs.is_contiguous(), "rope_cs must be contiguous fp32 [max_pos, 64, 2]")
-    return rope_cs, rope_cs.shape[0]
+    return rope_cs, s[0]
 
 
 def kv_write(kv_cache: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
@@ -179,15 +184,17 @@ def decode_paged(q: torch.Tensor, kv_cache: torch.Tensor, page_table: torch.Tens
     per-key rule), None for window OFF."""
     _need_gpu(q, kv_cache, page_table, seq_lens, rope_cs)
     _check_cache(kv_cache)
-    _need(q.dtype == torch.bfloat16 and q.dim() == 3 and q.shape[-1] == _lib.HEAD_DIM,
-          "q must be bf16 [B, Hq, 128]")
+    qs = q.shape
+    _need(q.dtype == torch.bfloat16 and len(qs) == 3 and qs[2] == _lib.HEAD_DIM, "q must be bf16 [B, Hq, 128]")
     q_sb, q_sh, q_sd = q.stride()
     _need(q_sd == 1, "last dim of q must be contiguous")
-    B, Hq, _ = q.shape
+    B, Hq = qs[0], qs[1]
     _need(seq_lens.dtype == torch.int32 and seq_lens.numel() == B, "seq_lens must be int32 [B]")
-    _need(page_table.dtype == torch.int32 and page_table.dim() == 2 and page_table.shape[0] == B
-          and page_table.is_contiguous(), "page_table must be contiguous int32 [B, max_pages]")
-    num_pages, hkv = kv_cache.shape[0], kv_cache.shape[1]
+    ps = page_table.shape
+    _need(page_table.dtype == torch.int32 and len(ps) == 2 and ps[0] == B and page_table.is_contiguous(),
+          "page_table must be contiguous int32 [B, max_pages]")
+    ks = kv_cache.shape
+    num_pages, hkv = ks[0], ks[1]
     rope_cs, max_pos = _rope(rope_cs)
     L = _lib.lib()
     dev = q.device
@@ -201,7 +208,7 @@ def decode_paged(q: torch.Tensor, kv_cache: torch.Tensor, page_table: torch.Tens
         seq_lens = seq_lens.contiguous()
     _lib.check(entry(
         out.data_ptr(), Hq * _lib.HEAD_DIM, _lib.HEAD_DIM, q.data_ptr(), q_sb, q_sh,
-        kv_cache.data_ptr(), num_pages, page_table.data_ptr(), page_table.shape[1],
+        kv_cache.data_ptr(), num_pages, page_table.data_ptr(), ps[1],
         seq_lens.data_ptr(), B, Hq, hkv, int(max_seq_len), table, float(sm_scale),
         _lib.ptr(rope_cs), max_pos, _layout(layout), ws[0], ws[1], stream))
     return out

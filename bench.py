@@ -41,7 +41,11 @@ decode    besides the eager back-to-back figure, every decode configuration is
           also replayed from a HIP graph (`*_graph_us`): the GPU time without
           the host's per-call work, which sets an eager loop's pace at short
           contexts; the Llama decode configurations are also timed through
-          prepared plans (`*_plan_us`, ops.DecodePlan, a serving loop's form).
+          prepared plans (`*_plan_us`, ops.DecodePlan, a serving loop's form),
+          and their eager and planned OFF and k = 2 batches are interleaved.
+          The Llama prefill and the 32K chunked prefill follow the
+          reference's per-call protocol (10 warm-up calls, an event pair per
+          call over about 0.3 s of calls, 10 to 200, median).
 detail    the other published configurations (Llama-3.2-3B prefill and decode,
           Qwen2.5-7B chunked prefill to 512K and decode at 512K), the 128K
           decode with other page arrangements (a sequence's pages scattered
@@ -222,6 +226,22 @@ def _events_time_median(fn, n, parts=5):
     call): where the host's launch work sets the pace (short contexts), one
     batch carries whatever the host was doing meanwhile."""
     return sorted(_events_time_batch(fn, max(1, n // parts)) for _ in range(parts))[parts // 2]
+
+
+def _events_time_interleaved(fns, n, parts=5):
+    """_events_time_median for several calls at once, their batches interleaved
+    (round i times one batch of each, in an order that rotates from round to
+    round): where the host sets the pace, its speed drifts over seconds, and
+    timing one call's batches before the other's would put that drift into
+    their ratio.  Returns {name: ms per call}."""
+    names = list(fns)
+    per = max(1, n // parts)
+    ts = {k: [] for k in names}
+    for i in range(parts):
+        for j in range(len(names)):
+            k = names[(i + j) % len(names)]
+            ts[k].append(_events_time_batch(fns[k], per))
+    return {k: sorted(v)[parts // 2] for k, v in ts.items()}
 
 
 def _graph_time(fn, calls, reps=5):
@@ -434,9 +454,17 @@ def bench_detail(steps=3):
     dev = torch.device("cuda:0")
     out = {"llama_prefill": {}, "llama_decode": {}, "qwen_prefill_chunked": {}}
 
-    def med(fn, n):
-        for _ in range(2):
+    def med(fn, target_s=0.3):
+        # the reference's per-call protocol (microbench/b1_bench_protocol.py:78-100):
+        # 10 warm-up calls, then one event pair per call over an adaptive count
+        # (here about target_s of calls, 10 to 200), median
+        for _ in range(10):
             fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        fn()
+        torch.cuda.synchronize()
+        n = max(10, min(200, int(target_s / max(time.perf_counter() - t0, 1e-6))))
         return statistics.median(_events_time(fn, n))
 
     # ---- Llama-3.2-3B prefill (attention kernel on a pre-packed cache) ----
@@ -450,7 +478,7 @@ def bench_detail(steps=3):
         kvc, table = interface.pack_kv(k, v, rope=rt)
         r = {}
         for name, zhi in (("off", None), ("k2", list(AW.window_zhi_from_kret(D, base, 2.0, 1 << 23)))):
-            r[name + "_ms"] = med(lambda: ops.prefill(q, kvc, table, N, 0, zhi, D ** -0.5, rt, 0), steps)
+            r[name + "_ms"] = med(lambda: ops.prefill(q, kvc, table, N, 0, zhi, D ** -0.5, rt, 0))
         r["on_over_off"] = r["off_ms"] / r["k2_ms"]
         r.update(_ref_ratio("llama_prefill_ms", N))
         out["llama_prefill"][N] = r
@@ -481,28 +509,33 @@ def bench_detail(steps=3):
             q = torch.randn((B, hq, D), generator=g, device=dev).to(torch.bfloat16)
             seq = torch.full((B,), N, dtype=torch.int32, device=dev)
             r = {"kv_pool_bytes": copies * B * pages * hkv * 8192}
+            eager, planned, plans = {}, {}, {}
             for name, zhi in (("off", None), ("k2", tuple(AW.window_zhi_from_kret(D, base, 2.0, 1 << 23)))):
                 it = [0]
 
-                def fn():
+                def fn(zhi=zhi, it=it):
                     t = tables[it[0] % copies]
                     it[0] += 1
                     return ops.decode_paged(q, pool.kv, t, seq, N, zhi, D ** -0.5, rt, 0)
                 for _ in range(10):
                     fn()
-                r[name + "_us"] = _events_time_median(fn, 40 * steps) * 1e3
                 r[name + "_graph_us"] = _graph_time(fn, 8 * copies) * 1e3
                 # the same calls through a prepared plan per pool copy (ops.DecodePlan: the
                 # serving loop's form, a few microseconds of host work per call)
-                plans = [ops.DecodePlan(pool.kv, t, seq, N, zhi, D ** -0.5, rt, 0, hq) for t in tables]
+                plans[name] = [ops.DecodePlan(pool.kv, t, seq, N, zhi, D ** -0.5, rt, 0, hq) for t in tables]
 
-                def fp():
-                    p = plans[it[0] % copies]
+                def fp(ps=plans[name], it=it):
+                    p = ps[it[0] % copies]
                     it[0] += 1
                     return p.run(q)
                 for _ in range(10):
                     fp()
-                r[name + "_plan_us"] = _events_time_median(fp, 40 * steps) * 1e3
+                eager[name], planned[name] = fn, fp
+            # eager and planned calls timed with the two windows' batches interleaved
+            for k, ms in _events_time_interleaved(eager, 40 * steps).items():
+                r[k + "_us"] = ms * 1e3
+            for k, ms in _events_time_interleaved(planned, 40 * steps).items():
+                r[k + "_plan_us"] = ms * 1e3
             r["on_over_off"] = r["off_us"] / r["k2_us"]
             r["on_over_off_graph"] = r["off_graph_us"] / r["k2_graph_us"]
             r["on_over_off_plan"] = r["off_plan_us"] / r["k2_plan_us"]
@@ -514,7 +547,7 @@ def bench_detail(steps=3):
                   f"{r['on_over_off_plan']:.3f}x; graph replay off {r['off_graph_us']:.1f} k2 {r['k2_graph_us']:.1f} us, "
                   f"{r['on_over_off_graph']:.3f}x" + (f"; reference {r['reference_ratio']:.3f}x)" if B == 1 else ")"),
                   flush=True)
-            del pool, tables, q, rt, plans
+            del pool, tables, q, rt, plans, eager, planned
             torch.cuda.empty_cache()
 
     # ---- Qwen2.5-7B prefill of 32K, 262K and 512K tokens in 8K query chunks ----
@@ -532,8 +565,11 @@ def bench_detail(steps=3):
             def fn():
                 for c0 in range(0, N, C):
                     ops.prefill(q[:, c0:c0 + C], kvc, table, c0 + C, c0, zhi, D ** -0.5, rt, 0)
-            fn()
-            r[name + "_ms"] = statistics.median(_events_time(fn, 2))
+            if N <= 32768:
+                r[name + "_ms"] = med(fn)
+            else:  # 0.4 s and 1.6 s per pass: two timed passes after one warm-up
+                fn()
+                r[name + "_ms"] = statistics.median(_events_time(fn, 2))
         r["on_over_off"] = r["off_ms"] / r["k2_ms"]
         r.update(_ref_ratio("qwen_prefill_ms", N))
         r["reference_note"] = "reference: single-shot FA4 (its stock OFF degrades past 256K)"
