@@ -44,6 +44,10 @@ CASES = [
     ("odd_tiles_150", 1, 150, 8, 2, 1e4, 2.0, True),
     ("odd_tiles_700_off", 1, 700, 8, 2, 1e4, None, True),
     ("odd_tiles_320_b2", 2, 320, 28, 4, 1e7, 64.0, True),
+    # 20 query tiles: three rounds of 8 over the XCDs, the last one partial, in
+    # the serpentine XCD order (the plain one would leave one XCD 36% above the
+    # mean causal work), two sequences
+    ("serpentine_5000_b2", 2, 5000, 8, 2, 1e4, 2.0, True),
 ]
 
 
