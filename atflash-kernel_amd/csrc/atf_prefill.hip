@@ -906,7 +906,8 @@ hipError_t ensure_lds_attribute() {
 // the busiest XCD's causal work (the k-tiles of its workgroups) more than 1%
 // above the mean, the order alternates (same-box A/B, outputs bitwise equal:
 // Llama-3.2-3B shape single shot, 8K -9 to -11%, 32K -2 to -3.6%; Qwen2.5-7B
-// shape 32K in 8K chunks -1 to -1.5%; 128K single shot within noise).  Where
+// shape 32K in 8K chunks -1 to -1.5%; 128K single shot OFF -0.4 to -0.5%,
+// k=2 -0.2 to +0.1% over 11 to 15 interleaved repetitions).  Where
 // the tiles' work is nearly equal (a late chunk of a chunked prefill, whose
 // keys are mostly the cached prefix) the plain order is kept: there the
 // serpentine one measured 0 to 1% slower (Qwen2.5-7B shape, 256K in 8K chunks).
