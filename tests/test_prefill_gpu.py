@@ -48,6 +48,9 @@ CASES = [
     # the serpentine XCD order (the plain one would leave one XCD 36% above the
     # mean causal work), two sequences
     ("serpentine_5000_b2", 2, 5000, 8, 2, 1e4, 2.0, True),
+    # GQA groups of 16 (32 q heads on 2 kv heads) and 7 over 14 q heads
+    ("g16_k2", 1, 1100, 32, 2, 1e6, 2.0, True),
+    ("hq14_g7_off", 1, 900, 14, 2, 1e6, None, True),
 ]
 
 
